@@ -1,0 +1,131 @@
+"""ctypes binding of libaegkv.so (declared in include/aegkv.h).
+
+torch is imported first on purpose: torch ships its own HIP runtime with the
+same SONAME (libamdhip64.so.7) as the system one, and loading torch first
+makes libaegkv bind to that runtime, so torch's streams and device pointers
+are valid inside the library.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede loading libaegkv, see module doc)
+
+LIB_PATH = Path(__file__).resolve().parent / "libaegkv.so"
+
+ABI_VERSION = 1
+
+OK = 0
+EINVAL = -1
+ERANGE = -2
+EDUP = -3
+EEXTENT = -4
+EOVERLAP = -5
+ENOMEM = -6
+
+MODE_AUTO = 0
+MODE_DIRECT = 1
+MODE_STAGED = 2
+
+TUNE_WGS_PER_CU = 1
+TUNE_STAGING_BYTES = 2
+TUNE_AUTO_D2H = 3
+TUNE_AUTO_H2D = 4
+TUNE_NT_STORES = 5
+
+#: every symbol include/aegkv.h declares
+EXPORTED_SYMBOLS = (
+    "aegkv_abi_version",
+    "aegkv_last_error",
+    "aegkv_tune",
+    "aegkv_swap",
+    "aegkv_swap_blocks",
+    "aegkv_copy_blocks",
+    "aegkv_host_alloc",
+    "aegkv_host_free",
+)
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int32
+_INT = ctypes.c_int
+_I64P = ctypes.POINTER(ctypes.c_int64)
+_I32P = ctypes.POINTER(ctypes.c_int32)
+_U64P = ctypes.POINTER(ctypes.c_uint64)
+_PP = ctypes.POINTER(ctypes.c_void_p)
+
+_SIGNATURES = {
+    "aegkv_abi_version": (_INT, []),
+    "aegkv_last_error": (ctypes.c_char_p, []),
+    "aegkv_tune": (_I64, [_INT, _I64]),
+    "aegkv_swap": (_INT, [_I64P, _I64P, _I64, _INT, _P, _I64, _P, _I64, _I64, _INT, _P]),
+    "aegkv_swap_blocks": (
+        _INT,
+        [_I32, _PP, _I64P, _I64P, _U64P, _I64, _I32, _I64P, _P, _I64, _I64, _I64, _I64,
+         _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P],
+    ),
+    "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_host_alloc": (_INT, [_PP, _I64]),
+    "aegkv_host_free": (_INT, [_P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class AegkvError(RuntimeError):
+    """A HIP runtime failure inside libaegkv (positive status)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"libaegkv status {status}: {message}")
+        self.status = status
+
+
+def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
+    """Load libaegkv.so once; raise if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path is not None else LIB_PATH
+        if not p.exists():
+            raise ImportError(
+                f"{p} is missing: build the HIP library first "
+                "(python -c 'import __graft_entry__ as g; g.build()')"
+            )
+        lib = ctypes.CDLL(str(p))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.aegkv_abi_version()
+        if ver != ABI_VERSION:
+            raise ImportError(f"libaegkv ABI {ver} != expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(status: int) -> None:
+    """Map a libaegkv status to the reference's Python exception types.
+
+    Invalid metadata raises ValueError (as aegaeon/worker.py:2237-2246 does),
+    HIP failures raise RuntimeError (as torch does for CUDA errors).
+    """
+    if status == OK:
+        return
+    msg = load().aegkv_last_error().decode(errors="replace")
+    if status < 0:
+        raise ValueError(msg)
+    raise AegkvError(status, msg)
+
+
+def tune(key: int, value: int = -1) -> int:
+    """Set a tuning knob (value >= 0) and return its previous value."""
+    prev = load().aegkv_tune(key, value)
+    if prev < 0:
+        check(int(prev))
+    return int(prev)

@@ -1,0 +1,918 @@
+// libaegkv: KV-cache block movement for MI355X (gfx950).
+//
+// Three operations, all pure byte movement (no arithmetic on the payload):
+//   * swap-out  : device K/V tiles -> composite pages of a pinned host pool
+//   * swap-in   : composite host pages -> device K/V tiles
+//   * copy_blocks: device block -> device block, every backing tensor
+//
+// One persistent "tile mover" kernel family does all of it. A work item is
+// one 16 B-per-lane chunk of one (entry, segment) tile; a workgroup of 256
+// lanes moves CHUNK = 256 * 16 * UNROLL bytes per item with all UNROLL loads
+// issued before the first store. Items are entry-major so consecutive items
+// walk one composite host page in address order (good for PCIe write
+// combining and host DRAM pages); the grid is a fixed number of workgroups
+// per CU that stride over the item space.
+//
+// Two host-transfer designs share the kernel:
+//   DIRECT: the "host side" pointer is the pinned host pool itself (mapped
+//           into the GPU address space by hipHostMalloc); the kernel's
+//           loads/stores cross PCIe.
+//   STAGED: the "host side" pointer is a contiguous device staging buffer
+//           laid out like the host pages; SDMA hipMemcpyAsync moves merged
+//           runs between staging and the host pool.
+//
+// Entry-point contracts are in include/aegkv.h.
+
+#include <hip/hip_runtime.h>
+#include "aegkv.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <map>
+#include <mutex>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------- errors --
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(static_cast<int>(e), "%s failed: %s (%d)", what, hipGetErrorString(e),
+              static_cast<int>(e));
+}
+
+#define AEGKV_HIP(call)                          \
+  do {                                           \
+    hipError_t e_ = (call);                      \
+    if (e_ != hipSuccess) return hip_fail(e_, #call); \
+  } while (0)
+
+// --------------------------------------------------------------- tunables --
+
+struct Tunables {
+  int64_t wgs_per_cu = 8;
+  int64_t staging_bytes = int64_t(512) << 20;
+  int64_t auto_d2h = AEGKV_MODE_DIRECT;
+  int64_t auto_h2d = AEGKV_MODE_DIRECT;
+  int64_t nt_stores = 1;
+};
+Tunables g_tune;
+std::mutex g_tune_mu;
+
+Tunables tunables() {
+  std::lock_guard<std::mutex> lk(g_tune_mu);
+  return g_tune;
+}
+
+// ------------------------------------------------------ device descriptors --
+
+constexpr int kWG = 256;    // lanes per workgroup (4 wavefronts of 64)
+constexpr int kUnroll = 4;  // 16 B loads in flight per lane per item
+constexpr int64_t kChunk = int64_t(kWG) * 16 * kUnroll;  // 16 KiB per item
+
+struct SegDesc {            // one backing tensor
+  char* base;
+  int64_t page_bytes;
+  int64_t host_offset;
+  uint64_t owner_mask;
+};
+static_assert(sizeof(SegDesc) == 32, "SegDesc layout");
+
+struct EntDesc {            // one swap entry, already resolved to sides
+  int64_t dev_block;        // block id in every backing tensor
+  int64_t host_slot;        // host block id (DIRECT) or staging slot (STAGED)
+  int32_t group;
+  int32_t first;            // first kernel block of the extent
+  int32_t valid;            // kernel blocks in the extent
+  int32_t pad;
+};
+static_assert(sizeof(EntDesc) == 32, "EntDesc layout");
+
+struct PairDesc {
+  int64_t src;
+  int64_t dst;
+};
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) v4u gv4u;  // global (VM) address space
+typedef __attribute__((address_space(1))) char gchar;
+
+// Move nbytes (multiple of 16, at most kChunk) with 16 B per lane. A full
+// chunk issues all kUnroll loads back to back before any store; only a
+// tail chunk pays for per-load guards.
+template <bool NT_STORE>
+__device__ __forceinline__ void move_chunk16(const char* src, char* dst, uint32_t nbytes) {
+  const gv4u* s = (const gv4u*)src;  // generic -> global address space
+  gv4u* d = (gv4u*)dst;
+  const uint32_t tid = threadIdx.x;
+  v4u r[kUnroll];
+  if (nbytes == static_cast<uint32_t>(kChunk)) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) r[u] = __builtin_nontemporal_load(s + tid + u * kWG);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (NT_STORE)
+        __builtin_nontemporal_store(r[u], d + tid + u * kWG);
+      else
+        d[tid + u * kWG] = r[u];
+    }
+    return;
+  }
+  const uint32_t n16 = nbytes >> 4;
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t i = tid + u * kWG;
+    if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t i = tid + u * kWG;
+    if (i < n16) {
+      if (NT_STORE)
+        __builtin_nontemporal_store(r[u], d + i);
+      else
+        d[i] = r[u];
+    }
+  }
+}
+
+// Byte-granular fallback for callers whose offsets are not 16 B aligned.
+__device__ __forceinline__ void move_chunk_bytes(const char* src, char* dst, uint32_t nbytes) {
+  const gchar* s = (const gchar*)src;
+  gchar* d = (gchar*)dst;
+  for (uint32_t i = threadIdx.x; i < nbytes; i += kWG) d[i] = s[i];
+}
+
+// Swap tile mover. Item w -> (entry e, segment s, chunk c), entry-major.
+// TO_HOST: device tile -> host side; otherwise host side -> device tile.
+// The host checks num_items < 2^32 so item decoding stays 32-bit.
+template <bool TO_HOST, bool VEC, bool NT_STORE>
+__global__ __launch_bounds__(kWG) void swap_tiles_kernel(
+    const SegDesc* __restrict__ segs, const EntDesc* __restrict__ ents,
+    const int64_t* __restrict__ kpp, uint32_t num_segs, uint32_t num_items,
+    uint32_t chunks_per_tile, char* host_base, int64_t host_stride, int64_t host_rank_offset) {
+  for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
+    const uint32_t tile = w / chunks_per_tile;
+    const uint32_t c = w - tile * chunks_per_tile;
+    const uint32_t e = tile / num_segs;
+    const uint32_t s = tile - e * num_segs;
+    const EntDesc ent = ents[e];
+    const SegDesc seg = segs[s];
+    if (!((seg.owner_mask >> ent.group) & 1ull)) continue;
+    const int64_t unit = seg.page_bytes / kpp[ent.group];
+    const int64_t off = unit * ent.first;
+    const int64_t len = unit * ent.valid;
+    const int64_t begin = static_cast<int64_t>(c) * kChunk;
+    if (begin >= len) continue;
+    const uint32_t nbytes = static_cast<uint32_t>((len - begin < kChunk) ? (len - begin) : kChunk);
+    char* dev = seg.base + ent.dev_block * seg.page_bytes + off + begin;
+    char* host = host_base + ent.host_slot * host_stride + host_rank_offset +
+                 seg.host_offset + off + begin;
+    const char* src = TO_HOST ? dev : host;
+    char* dst = TO_HOST ? host : dev;
+    if (VEC)
+      move_chunk16<NT_STORE>(src, dst, nbytes);
+    else
+      move_chunk_bytes(src, dst, nbytes);
+  }
+}
+
+// copy_blocks: item w -> (pair p, segment s, chunk c), pair-major.
+template <bool VEC, bool NT_STORE>
+__global__ __launch_bounds__(kWG) void copy_blocks_kernel(
+    const SegDesc* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
+    uint32_t num_items, uint32_t chunks_per_tile) {
+  for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
+    const uint32_t tile = w / chunks_per_tile;
+    const uint32_t c = w - tile * chunks_per_tile;
+    const uint32_t p = tile / num_segs;
+    const uint32_t s = tile - p * num_segs;
+    const PairDesc pr = pairs[p];
+    const SegDesc seg = segs[s];
+    const int64_t begin = static_cast<int64_t>(c) * kChunk;
+    if (begin >= seg.page_bytes) continue;
+    const uint32_t nbytes = static_cast<uint32_t>(
+        (seg.page_bytes - begin < kChunk) ? (seg.page_bytes - begin) : kChunk);
+    const char* src = seg.base + pr.src * seg.page_bytes + begin;
+    char* dst = seg.base + pr.dst * seg.page_bytes + begin;
+    if (VEC)
+      move_chunk16<NT_STORE>(src, dst, nbytes);
+    else
+      move_chunk_bytes(src, dst, nbytes);
+  }
+}
+
+// ------------------------------------------------------- per-device state --
+
+// Stream-ordered pinned->device upload ring for call descriptors. A region
+// is reused only after the event recorded behind the call that read it has
+// completed, whatever stream that call ran on.
+struct Ring {
+  char* host = nullptr;
+  char* dev = nullptr;
+  size_t cap = 0;
+  size_t head = 0;
+  struct Region {
+    size_t begin, end;
+    hipEvent_t ev;
+  };
+  std::deque<Region> inflight;
+  std::vector<hipEvent_t> spare;
+};
+
+struct DeviceCtx {
+  int device = -1;
+  int num_cus = 0;
+  std::mutex mu;
+  Ring ring;
+};
+
+std::mutex g_ctx_mu;
+std::map<int, DeviceCtx*> g_ctx;
+
+std::mutex g_host_mu;
+std::map<uintptr_t, size_t> g_host_allocs;  // pools from aegkv_host_alloc
+
+int get_ctx(DeviceCtx** out) {
+  int dev = -1;
+  AEGKV_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(g_ctx_mu);
+  auto it = g_ctx.find(dev);
+  if (it != g_ctx.end()) {
+    *out = it->second;
+    return 0;
+  }
+  auto* ctx = new DeviceCtx();
+  ctx->device = dev;
+  AEGKV_HIP(hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (ctx->num_cus <= 0) ctx->num_cus = 1;
+  // Keep stream-ordered staging memory cached in the pool between calls.
+  hipMemPool_t pool = nullptr;
+  if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess && pool) {
+    uint64_t threshold = UINT64_MAX;
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &threshold);
+  }
+  (void)hipGetLastError();
+  g_ctx[dev] = ctx;
+  *out = ctx;
+  return 0;
+}
+
+int ring_grow(Ring& r, size_t need) {
+  // Retire everything, then replace the buffers.
+  for (auto& reg : r.inflight) {
+    AEGKV_HIP(hipEventSynchronize(reg.ev));
+    r.spare.push_back(reg.ev);
+  }
+  r.inflight.clear();
+  if (r.host) AEGKV_HIP(hipHostFree(r.host));
+  if (r.dev) AEGKV_HIP(hipFree(r.dev));
+  r.host = nullptr;
+  r.dev = nullptr;
+  size_t cap = size_t(4) << 20;
+  while (cap < need) cap <<= 1;
+  AEGKV_HIP(hipHostMalloc(reinterpret_cast<void**>(&r.host), cap, hipHostMallocDefault));
+  AEGKV_HIP(hipMalloc(reinterpret_cast<void**>(&r.dev), cap));
+  r.cap = cap;
+  r.head = 0;
+  return 0;
+}
+
+// Reserve `bytes` of the ring (caller holds ctx->mu). Returns offset.
+int ring_reserve(Ring& r, size_t bytes, size_t* offset) {
+  bytes = (bytes + 255) & ~size_t(255);
+  if (bytes == 0) bytes = 256;
+  if (bytes > r.cap) {
+    int rc = ring_grow(r, bytes);
+    if (rc) return rc;
+  }
+  // Retire completed regions without blocking.
+  while (!r.inflight.empty() && hipEventQuery(r.inflight.front().ev) == hipSuccess) {
+    r.spare.push_back(r.inflight.front().ev);
+    r.inflight.pop_front();
+  }
+  size_t start = r.head;
+  if (start + bytes > r.cap) start = 0;
+  const size_t end = start + bytes;
+  auto overlaps = [&](const Ring::Region& g) { return g.begin < end && start < g.end; };
+  for (;;) {
+    bool any = false;
+    for (auto& g : r.inflight)
+      if (overlaps(g)) {
+        any = true;
+        break;
+      }
+    if (!any) break;
+    AEGKV_HIP(hipEventSynchronize(r.inflight.front().ev));
+    r.spare.push_back(r.inflight.front().ev);
+    r.inflight.pop_front();
+  }
+  r.head = end;
+  *offset = start;
+  return 0;
+}
+
+int ring_commit(Ring& r, size_t offset, size_t bytes, hipStream_t stream) {
+  bytes = (bytes + 255) & ~size_t(255);
+  if (bytes == 0) bytes = 256;
+  hipEvent_t ev;
+  if (!r.spare.empty()) {
+    ev = r.spare.back();
+    r.spare.pop_back();
+  } else {
+    AEGKV_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
+  hipError_t e = hipEventRecord(ev, stream);
+  if (e != hipSuccess) {
+    r.spare.push_back(ev);
+    return hip_fail(e, "hipEventRecord");
+  }
+  r.inflight.push_back({offset, offset + bytes, ev});
+  return 0;
+}
+
+// ------------------------------------------------------------- validation --
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks [ptr, ptr + bytes) lies inside one HIP device allocation.
+int check_device_range(const void* ptr, int64_t bytes, const char* what) {
+  if (bytes == 0) return 0;
+  void* base = nullptr;
+  size_t size = 0;
+  hipError_t e = hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr));
+  if (e != hipSuccess || base == nullptr) {
+    (void)hipGetLastError();
+    return fail(AEGKV_EINVAL, "%s (%p) is not HIP device memory", what, ptr);
+  }
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
+  if (p < b || p + static_cast<uint64_t>(bytes) > b + size)
+    return fail(AEGKV_ERANGE, "%s: %lld bytes at %p exceed its allocation (%zu bytes at %p)",
+                what, static_cast<long long>(bytes), ptr, size, base);
+  return 0;
+}
+
+// Checks a host pool is pinned and device-visible; kernels dereference it
+// directly in DIRECT mode.
+int check_host_range(const void* ptr, int64_t bytes, const char* what) {
+  if (bytes == 0) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    auto it = g_host_allocs.upper_bound(reinterpret_cast<uintptr_t>(ptr));
+    if (it != g_host_allocs.begin()) {
+      --it;
+      const uintptr_t b = it->first;
+      const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
+      if (p >= b && p < b + it->second) {
+        if (p + static_cast<uint64_t>(bytes) > b + it->second)
+          return fail(AEGKV_ERANGE, "%s: %lld bytes at %p exceed its pinned pool", what,
+                      static_cast<long long>(bytes), ptr);
+        return 0;
+      }
+    }
+  }
+  hipPointerAttribute_t attr;
+  std::memset(&attr, 0, sizeof(attr));
+  hipError_t e = hipPointerGetAttributes(&attr, ptr);
+  if (e != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();
+    return fail(AEGKV_EINVAL, "%s (%p) is not pinned host memory (use aegkv_host_alloc)",
+                what, ptr);
+  }
+  return 0;
+}
+
+// ----------------------------------------------------------- launching --
+
+int64_t grid_for(const DeviceCtx* ctx, int64_t items) {
+  const Tunables t = tunables();
+  int64_t g = static_cast<int64_t>(ctx->num_cus) * std::max<int64_t>(1, t.wgs_per_cu);
+  return std::max<int64_t>(1, std::min<int64_t>(g, items));
+}
+
+template <bool TO_HOST, bool VEC, bool NT>
+hipError_t launch_swap_t(int64_t grid, hipStream_t st, const SegDesc* s, const EntDesc* e,
+                         const int64_t* k, uint32_t ns, uint32_t items, uint32_t cpt, char* hb,
+                         int64_t hs, int64_t hro) {
+  hipLaunchKernelGGL((swap_tiles_kernel<TO_HOST, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(kWG), 0, st, s, e, k, ns, items, cpt, hb, hs, hro);
+  return hipGetLastError();
+}
+
+hipError_t launch_swap(bool to_host, bool vec, bool nt, int64_t grid, hipStream_t st,
+                       const SegDesc* s, const EntDesc* e, const int64_t* k, uint32_t ns,
+                       uint32_t items, uint32_t cpt, char* hb, int64_t hs, int64_t hro) {
+#define AEGKV_L(A, B, C) \
+  return launch_swap_t<A, B, C>(grid, st, s, e, k, ns, items, cpt, hb, hs, hro)
+  if (to_host) {
+    if (vec) {
+      if (nt) AEGKV_L(true, true, true);
+      AEGKV_L(true, true, false);
+    }
+    AEGKV_L(true, false, false);
+  }
+  if (vec) {
+    if (nt) AEGKV_L(false, true, true);
+    AEGKV_L(false, true, false);
+  }
+  AEGKV_L(false, false, false);
+#undef AEGKV_L
+}
+
+hipError_t launch_copy(bool vec, bool nt, int64_t grid, hipStream_t st, const SegDesc* s,
+                       const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
+  const dim3 g(static_cast<uint32_t>(grid)), b(kWG);
+  if (vec) {
+    if (nt)
+      hipLaunchKernelGGL((copy_blocks_kernel<true, true>), g, b, 0, st, s, p, ns, items, cpt);
+    else
+      hipLaunchKernelGGL((copy_blocks_kernel<true, false>), g, b, 0, st, s, p, ns, items, cpt);
+  } else {
+    hipLaunchKernelGGL((copy_blocks_kernel<false, false>), g, b, 0, st, s, p, ns, items, cpt);
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------ swap core --
+
+struct SwapLayout {
+  int32_t num_segments;
+  void* const* bases;
+  const int64_t* page_bytes;
+  const int64_t* host_offsets;
+  const uint64_t* owner_masks;
+  int64_t device_num_blocks;
+  int32_t num_groups;
+  const int64_t* kpp;
+  char* host_pool;
+  int64_t host_num_blocks;
+  int64_t host_page_bytes;
+  int64_t host_rank_offset;
+};
+
+struct SwapList {
+  int64_t n;
+  const int64_t* src;
+  const int64_t* dst;
+  const int32_t* group;     // may be null: all group 0
+  const int64_t* first;     // may be null: all 0
+  const int64_t* valid;     // may be null: all kpp[group]
+};
+
+// dev_vec: every device tile extent is 16 B aligned; host_vec: so is every
+// host-pool extent. The 16 B kernel path needs both sides aligned.
+int validate_layout(const SwapLayout& L, bool direct, int64_t* composite_bytes,
+                    bool* dev_vec, bool* host_vec) {
+  if (L.num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
+  if (!L.bases || !L.page_bytes || !L.host_offsets || !L.owner_masks)
+    return fail(AEGKV_EINVAL, "segment arrays must not be null");
+  if (L.device_num_blocks <= 0) return fail(AEGKV_EINVAL, "device_num_blocks must be positive");
+  if (L.num_groups <= 0 || L.num_groups > 64)
+    return fail(AEGKV_EINVAL, "num_groups must be in [1, 64], got %d", L.num_groups);
+  if (!L.kpp) return fail(AEGKV_EINVAL, "group_kernel_blocks_per_page must not be null");
+  if (!L.host_pool) return fail(AEGKV_EINVAL, "host_pool must not be null");
+  if (L.host_num_blocks <= 0 || L.host_page_bytes <= 0)
+    return fail(AEGKV_EINVAL, "host pool geometry must be positive");
+  if (L.host_rank_offset < 0) return fail(AEGKV_EINVAL, "host_rank_offset must be >= 0");
+  for (int32_t g = 0; g < L.num_groups; ++g)
+    if (L.kpp[g] <= 0)
+      return fail(AEGKV_EINVAL, "kernel_blocks_per_page[%d]=%lld must be positive", g,
+                  static_cast<long long>(L.kpp[g]));
+  bool v = true;
+  int64_t composite = 0;
+  for (int32_t s = 0; s < L.num_segments; ++s) {
+    const int64_t pb = L.page_bytes[s];
+    const int64_t ho = L.host_offsets[s];
+    if (!L.bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
+    if (pb <= 0) return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
+    if (ho < 0) return fail(AEGKV_EINVAL, "segment %d host offset must be >= 0", s);
+    if (L.host_rank_offset + ho + pb > L.host_page_bytes)
+      return fail(AEGKV_ERANGE,
+                  "segment %d [%lld, +%lld) at rank offset %lld overruns the %lld-byte host page",
+                  s, static_cast<long long>(ho), static_cast<long long>(pb),
+                  static_cast<long long>(L.host_rank_offset),
+                  static_cast<long long>(L.host_page_bytes));
+    if (L.owner_masks[s] == 0) return fail(AEGKV_EINVAL, "segment %d has no owning group", s);
+    for (int32_t g = 0; g < L.num_groups; ++g)
+      if (((L.owner_masks[s] >> g) & 1ull) && pb % L.kpp[g] != 0)
+        return fail(AEGKV_EEXTENT,
+                    "segment %d page of %lld bytes is not divisible by %lld kernel blocks", s,
+                    static_cast<long long>(pb), static_cast<long long>(L.kpp[g]));
+    if (L.num_groups < 64 && (L.owner_masks[s] >> L.num_groups) != 0)
+      return fail(AEGKV_ERANGE, "segment %d owner mask names a group >= %d", s, L.num_groups);
+    int rc = check_device_range(L.bases[s], L.device_num_blocks * pb, "segment base");
+    if (rc) return rc;
+    v = v && aligned16(L.bases[s]) && pb % 16 == 0 && ho % 16 == 0;
+    for (int32_t g = 0; g < L.num_groups && v; ++g)
+      if ((L.owner_masks[s] >> g) & 1ull) v = (pb / L.kpp[g]) % 16 == 0;
+    composite = std::max(composite, ho + pb);
+  }
+  if (direct) {
+    int rc = check_host_range(L.host_pool, L.host_num_blocks * L.host_page_bytes, "host_pool");
+    if (rc) return rc;
+  }
+  *composite_bytes = composite;
+  *dev_vec = v;
+  *host_vec = aligned16(L.host_pool) && L.host_page_bytes % 16 == 0 &&
+              L.host_rank_offset % 16 == 0;
+  return 0;
+}
+
+int validate_list(const SwapLayout& L, const SwapList& E, bool is_swap_in) {
+  if (E.n < 0) return fail(AEGKV_EINVAL, "num_entries must be >= 0");
+  if (E.n == 0) return 0;
+  if (!E.src || !E.dst) return fail(AEGKV_EINVAL, "block id arrays must not be null");
+  const int64_t src_lim = is_swap_in ? L.host_num_blocks : L.device_num_blocks;
+  const int64_t dst_lim = is_swap_in ? L.device_num_blocks : L.host_num_blocks;
+  std::vector<uint8_t> seen(static_cast<size_t>(dst_lim), 0);
+  for (int64_t i = 0; i < E.n; ++i) {
+    if (E.src[i] < 0 || E.src[i] >= src_lim)
+      return fail(AEGKV_ERANGE, "source block id %lld at %lld outside [0, %lld)",
+                  static_cast<long long>(E.src[i]), static_cast<long long>(i),
+                  static_cast<long long>(src_lim));
+    if (E.dst[i] < 0 || E.dst[i] >= dst_lim)
+      return fail(AEGKV_ERANGE, "target block id %lld at %lld outside [0, %lld)",
+                  static_cast<long long>(E.dst[i]), static_cast<long long>(i),
+                  static_cast<long long>(dst_lim));
+    if (seen[static_cast<size_t>(E.dst[i])])
+      return fail(AEGKV_EDUP, "target block id %lld appears twice",
+                  static_cast<long long>(E.dst[i]));
+    seen[static_cast<size_t>(E.dst[i])] = 1;
+    const int32_t g = E.group ? E.group[i] : 0;
+    if (g < 0 || g >= L.num_groups)
+      return fail(AEGKV_ERANGE, "group id %d at %lld outside [0, %d)", g,
+                  static_cast<long long>(i), L.num_groups);
+    const int64_t k = L.kpp[g];
+    const int64_t first = E.first ? E.first[i] : 0;
+    const int64_t valid = E.valid ? E.valid[i] : k;
+    if (first < 0 || valid < 0 || first + valid > k)
+      return fail(AEGKV_EEXTENT, "kernel-block extent [%lld, %lld) at %lld exceeds page size %lld",
+                  static_cast<long long>(first), static_cast<long long>(first + valid),
+                  static_cast<long long>(i), static_cast<long long>(k));
+  }
+  return 0;
+}
+
+struct Run {
+  int64_t host_off;   // byte offset inside the host pool
+  int64_t stage_off;  // byte offset inside staging
+  int64_t len;
+};
+
+// Enqueue one descriptor upload + kernel for entries [idx...] resolved to
+// the given host side. Caller holds ctx->mu.
+int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
+                        const std::vector<int64_t>& order, size_t lo, size_t hi,
+                        bool is_swap_in, bool staged, char* host_side, int64_t host_stride,
+                        int64_t host_rank_off, bool vec, hipStream_t stream) {
+  const int32_t S = L.num_segments;
+  const int64_t n = static_cast<int64_t>(hi - lo);
+  if (n == 0) return 0;
+  const size_t seg_bytes = sizeof(SegDesc) * S;
+  const size_t kpp_off = (seg_bytes + 255) & ~size_t(255);
+  const size_t kpp_bytes = sizeof(int64_t) * L.num_groups;
+  const size_t ent_off = (kpp_off + kpp_bytes + 255) & ~size_t(255);
+  const size_t total = ent_off + sizeof(EntDesc) * n;
+  size_t off = 0;
+  int rc = ring_reserve(ctx->ring, total, &off);
+  if (rc) return rc;
+  char* h = ctx->ring.host + off;
+  SegDesc* hs = reinterpret_cast<SegDesc*>(h);
+  int64_t max_page = 0;
+  for (int32_t s = 0; s < S; ++s) {
+    hs[s].base = static_cast<char*>(L.bases[s]);
+    hs[s].page_bytes = L.page_bytes[s];
+    hs[s].host_offset = L.host_offsets[s];
+    hs[s].owner_mask = L.owner_masks[s];
+    max_page = std::max(max_page, L.page_bytes[s]);
+  }
+  std::memcpy(h + kpp_off, L.kpp, kpp_bytes);
+  EntDesc* he = reinterpret_cast<EntDesc*>(h + ent_off);
+  for (int64_t j = 0; j < n; ++j) {
+    const int64_t i = order[lo + j];
+    const int32_t g = E.group ? E.group[i] : 0;
+    EntDesc d;
+    d.dev_block = is_swap_in ? E.dst[i] : E.src[i];
+    const int64_t host_id = is_swap_in ? E.src[i] : E.dst[i];
+    d.host_slot = staged ? j : host_id;
+    d.group = g;
+    d.first = static_cast<int32_t>(E.first ? E.first[i] : 0);
+    d.valid = static_cast<int32_t>(E.valid ? E.valid[i] : L.kpp[g]);
+    d.pad = 0;
+    he[j] = d;
+  }
+  char* dv = ctx->ring.dev + off;
+  const int64_t cpt = (max_page + kChunk - 1) / kChunk;
+  const int64_t items = n * S * cpt;
+  if (items >= (int64_t(1) << 32)) {
+    ctx->ring.head = off;  // nothing was enqueued; hand the region back
+    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
+                static_cast<long long>(items));
+  }
+  hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
+  const Tunables t = tunables();
+  e = launch_swap(!is_swap_in, vec, t.nt_stores != 0, grid_for(ctx, items), stream,
+                  reinterpret_cast<const SegDesc*>(dv),
+                  reinterpret_cast<const EntDesc*>(dv + ent_off),
+                  reinterpret_cast<const int64_t*>(dv + kpp_off), static_cast<uint32_t>(S),
+                  static_cast<uint32_t>(items), static_cast<uint32_t>(cpt), host_side,
+                  host_stride, host_rank_off);
+  if (e != hipSuccess) return hip_fail(e, "swap_tiles_kernel launch");
+  return ring_commit(ctx->ring, off, total, stream);
+}
+
+// Runs of host bytes one staged entry moves, merged when contiguous.
+void entry_runs(const SwapLayout& L, const SwapList& E, int64_t i, bool is_swap_in,
+                int64_t slot, int64_t composite, std::vector<Run>& runs) {
+  const int32_t g = E.group ? E.group[i] : 0;
+  const int64_t k = L.kpp[g];
+  const int64_t first = E.first ? E.first[i] : 0;
+  const int64_t valid = E.valid ? E.valid[i] : k;
+  const int64_t host_id = is_swap_in ? E.src[i] : E.dst[i];
+  const int64_t host_page = host_id * L.host_page_bytes + L.host_rank_offset;
+  const int64_t stage_page = slot * composite;
+  for (int32_t s = 0; s < L.num_segments; ++s) {
+    if (!((L.owner_masks[s] >> g) & 1ull)) continue;
+    const int64_t unit = L.page_bytes[s] / k;
+    const int64_t off = unit * first, len = unit * valid;
+    if (len == 0) continue;
+    const int64_t ho = host_page + L.host_offsets[s] + off;
+    const int64_t so = stage_page + L.host_offsets[s] + off;
+    if (!runs.empty()) {
+      Run& r = runs.back();
+      if (r.host_off + r.len == ho && r.stage_off + r.len == so) {
+        r.len += len;
+        continue;
+      }
+    }
+    runs.push_back({ho, so, len});
+  }
+}
+
+int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
+              hipStream_t stream) {
+  if (mode < AEGKV_MODE_AUTO || mode > AEGKV_MODE_STAGED)
+    return fail(AEGKV_EINVAL, "unknown transfer mode %d", mode);
+  const Tunables t = tunables();
+  if (mode == AEGKV_MODE_AUTO)
+    mode = static_cast<int>(is_swap_in ? t.auto_h2d : t.auto_d2h);
+  const bool staged = mode == AEGKV_MODE_STAGED;
+  int64_t composite = 0;
+  bool dev_vec = false, host_vec = false;
+  int rc = validate_layout(L, !staged, &composite, &dev_vec, &host_vec);
+  if (rc) return rc;
+  rc = validate_list(L, E, is_swap_in);
+  if (rc) return rc;
+  if (E.n == 0) return 0;
+  DeviceCtx* ctx = nullptr;
+  rc = get_ctx(&ctx);
+  if (rc) return rc;
+
+  std::vector<int64_t> order(static_cast<size_t>(E.n));
+  for (int64_t i = 0; i < E.n; ++i) order[static_cast<size_t>(i)] = i;
+
+  if (!staged) {
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    return enqueue_swap_kernel(ctx, L, E, order, 0, order.size(), is_swap_in, false,
+                               L.host_pool, L.host_page_bytes, L.host_rank_offset,
+                               dev_vec && host_vec, stream);
+  }
+
+  // STAGED: host-id order lets consecutive host pages merge into one DMA.
+  const int64_t* host_ids = is_swap_in ? E.src : E.dst;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t a, int64_t b) { return host_ids[a] < host_ids[b]; });
+  const int64_t per_chunk =
+      std::max<int64_t>(1, std::min<int64_t>(E.n, t.staging_bytes / composite));
+  // Staging comes from hipMallocAsync (256 B aligned) with a composite stride.
+  const bool vec_stage = dev_vec && composite % 16 == 0;
+  std::vector<Run> runs;
+  for (size_t lo = 0; lo < order.size(); lo += static_cast<size_t>(per_chunk)) {
+    const size_t hi = std::min(order.size(), lo + static_cast<size_t>(per_chunk));
+    const int64_t m = static_cast<int64_t>(hi - lo);
+    runs.clear();
+    for (size_t j = lo; j < hi; ++j)
+      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
+    void* staging = nullptr;
+    AEGKV_HIP(hipMallocAsync(&staging, static_cast<size_t>(m * composite), stream));
+    char* st = static_cast<char*>(staging);
+    if (is_swap_in) {
+      for (const Run& r : runs)
+        AEGKV_HIP(hipMemcpyAsync(st + r.stage_off, L.host_pool + r.host_off,
+                                 static_cast<size_t>(r.len), hipMemcpyHostToDevice, stream));
+    }
+    {
+      std::lock_guard<std::mutex> lk(ctx->mu);
+      rc = enqueue_swap_kernel(ctx, L, E, order, lo, hi, is_swap_in, true, st, composite, 0,
+                               vec_stage, stream);
+    }
+    if (rc) {
+      (void)hipFreeAsync(staging, stream);
+      return rc;
+    }
+    if (!is_swap_in) {
+      for (const Run& r : runs)
+        AEGKV_HIP(hipMemcpyAsync(L.host_pool + r.host_off, st + r.stage_off,
+                                 static_cast<size_t>(r.len), hipMemcpyDeviceToHost, stream));
+    }
+    AEGKV_HIP(hipFreeAsync(staging, stream));
+  }
+  return 0;
+}
+
+}  // namespace
+
+// =============================================================== C ABI ==
+
+extern "C" {
+
+int aegkv_abi_version(void) { return AEGKV_ABI_VERSION; }
+
+const char* aegkv_last_error(void) { return g_err; }
+
+int64_t aegkv_tune(int key, int64_t value) {
+  std::lock_guard<std::mutex> lk(g_tune_mu);
+  int64_t* slot = nullptr;
+  switch (key) {
+    case AEGKV_TUNE_WGS_PER_CU: slot = &g_tune.wgs_per_cu; break;
+    case AEGKV_TUNE_STAGING_BYTES: slot = &g_tune.staging_bytes; break;
+    case AEGKV_TUNE_AUTO_D2H: slot = &g_tune.auto_d2h; break;
+    case AEGKV_TUNE_AUTO_H2D: slot = &g_tune.auto_h2d; break;
+    case AEGKV_TUNE_NT_STORES: slot = &g_tune.nt_stores; break;
+    default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
+  }
+  const int64_t prev = *slot;
+  if (value >= 0) {
+    if ((key == AEGKV_TUNE_AUTO_D2H || key == AEGKV_TUNE_AUTO_H2D) &&
+        value != AEGKV_MODE_DIRECT && value != AEGKV_MODE_STAGED)
+      return fail(AEGKV_EINVAL, "AUTO must resolve to DIRECT or STAGED");
+    if (key == AEGKV_TUNE_WGS_PER_CU && (value < 1 || value > 64))
+      return fail(AEGKV_EINVAL, "workgroups per CU must be in [1, 64]");
+    if (key == AEGKV_TUNE_STAGING_BYTES && value < (int64_t(1) << 20))
+      return fail(AEGKV_EINVAL, "staging must be at least 1 MiB");
+    *slot = value;
+  }
+  return prev;
+}
+
+int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
+               int64_t num_ids, int is_swap_in, void* kv_cache, int64_t cache_num_blocks,
+               void* kv_swap, int64_t swap_num_blocks, int64_t block_bytes, int mode,
+               hipStream_t stream) {
+  g_err[0] = '\0';
+  if (block_bytes <= 0) return fail(AEGKV_EINVAL, "block_bytes must be positive");
+  void* bases[1] = {kv_cache};
+  const int64_t page[1] = {block_bytes};
+  const int64_t hoff[1] = {0};
+  const uint64_t owner[1] = {1};
+  const int64_t kpp[1] = {1};
+  SwapLayout L{1, bases, page, hoff, owner, cache_num_blocks, 1, kpp,
+               static_cast<char*>(kv_swap), swap_num_blocks, block_bytes, 0};
+  SwapList E{num_ids, source_block_ids, target_block_ids, nullptr, nullptr, nullptr};
+  return swap_core(L, E, is_swap_in != 0, mode, stream);
+}
+
+int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
+                      const int64_t* segment_page_bytes, const int64_t* segment_host_offsets,
+                      const uint64_t* segment_owner_masks, int64_t device_num_blocks,
+                      int32_t num_groups, const int64_t* group_kernel_blocks_per_page,
+                      void* host_pool, int64_t host_num_blocks, int64_t host_page_bytes,
+                      int64_t host_rank_offset, int64_t num_entries,
+                      const int64_t* source_block_ids, const int64_t* target_block_ids,
+                      const int32_t* group_ids, const int64_t* first_kernel_blocks,
+                      const int64_t* valid_kernel_blocks, int is_swap_in, int mode,
+                      hipStream_t stream) {
+  g_err[0] = '\0';
+  if (num_entries > 0 && (!group_ids || !first_kernel_blocks || !valid_kernel_blocks))
+    return fail(AEGKV_EINVAL, "entry metadata arrays must not be null");
+  SwapLayout L{num_segments, segment_bases, segment_page_bytes, segment_host_offsets,
+               segment_owner_masks, device_num_blocks, num_groups,
+               group_kernel_blocks_per_page, static_cast<char*>(host_pool), host_num_blocks,
+               host_page_bytes, host_rank_offset};
+  SwapList E{num_entries, source_block_ids, target_block_ids, group_ids, first_kernel_blocks,
+             valid_kernel_blocks};
+  return swap_core(L, E, is_swap_in != 0, mode, stream);
+}
+
+int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
+                      const int64_t* segment_page_bytes, int64_t device_num_blocks,
+                      int64_t num_pairs, const int64_t* src_block_ids,
+                      const int64_t* dst_block_ids, hipStream_t stream) {
+  g_err[0] = '\0';
+  if (num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
+  if (!segment_bases || !segment_page_bytes)
+    return fail(AEGKV_EINVAL, "segment arrays must not be null");
+  if (device_num_blocks <= 0) return fail(AEGKV_EINVAL, "device_num_blocks must be positive");
+  if (num_pairs < 0) return fail(AEGKV_EINVAL, "num_pairs must be >= 0");
+  if (num_pairs > 0 && (!src_block_ids || !dst_block_ids))
+    return fail(AEGKV_EINVAL, "block id arrays must not be null");
+  bool vec = true;
+  int64_t max_page = 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    if (!segment_bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
+    if (segment_page_bytes[s] <= 0)
+      return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
+    int rc = check_device_range(segment_bases[s], device_num_blocks * segment_page_bytes[s],
+                                "segment base");
+    if (rc) return rc;
+    vec = vec && aligned16(segment_bases[s]) && segment_page_bytes[s] % 16 == 0;
+    max_page = std::max(max_page, segment_page_bytes[s]);
+  }
+  // 0 = untouched, 1 = source, 2 = target
+  std::vector<uint8_t> role(static_cast<size_t>(device_num_blocks), 0);
+  for (int64_t i = 0; i < num_pairs; ++i) {
+    const int64_t s = src_block_ids[i], d = dst_block_ids[i];
+    if (s < 0 || s >= device_num_blocks || d < 0 || d >= device_num_blocks)
+      return fail(AEGKV_ERANGE, "pair %lld (%lld -> %lld) outside [0, %lld)",
+                  static_cast<long long>(i), static_cast<long long>(s),
+                  static_cast<long long>(d), static_cast<long long>(device_num_blocks));
+    if (role[static_cast<size_t>(d)] == 2)
+      return fail(AEGKV_EDUP, "target block id %lld appears twice", static_cast<long long>(d));
+    if (role[static_cast<size_t>(d)] == 1)
+      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
+                  static_cast<long long>(d));
+    role[static_cast<size_t>(d)] = 2;
+  }
+  for (int64_t i = 0; i < num_pairs; ++i) {
+    const int64_t s = src_block_ids[i];
+    if (role[static_cast<size_t>(s)] == 2)
+      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
+                  static_cast<long long>(s));
+    role[static_cast<size_t>(s)] = 1;
+  }
+  if (num_pairs == 0) return 0;
+  const int64_t cpt = (max_page + kChunk - 1) / kChunk;
+  const int64_t items = num_pairs * num_segments * cpt;
+  if (items >= (int64_t(1) << 32))
+    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
+                static_cast<long long>(items));
+  DeviceCtx* ctx = nullptr;
+  int rc = get_ctx(&ctx);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const size_t seg_bytes = sizeof(SegDesc) * num_segments;
+  const size_t pair_off = (seg_bytes + 255) & ~size_t(255);
+  const size_t total = pair_off + sizeof(PairDesc) * num_pairs;
+  size_t off = 0;
+  rc = ring_reserve(ctx->ring, total, &off);
+  if (rc) return rc;
+  char* h = ctx->ring.host + off;
+  SegDesc* hs = reinterpret_cast<SegDesc*>(h);
+  for (int32_t s = 0; s < num_segments; ++s)
+    hs[s] = SegDesc{static_cast<char*>(segment_bases[s]), segment_page_bytes[s], 0, ~0ull};
+  PairDesc* hp = reinterpret_cast<PairDesc*>(h + pair_off);
+  for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_block_ids[i], dst_block_ids[i]};
+  char* dv = ctx->ring.dev + off;
+  hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
+  const Tunables t = tunables();
+  e = launch_copy(vec, t.nt_stores != 0, grid_for(ctx, items), stream,
+                  reinterpret_cast<const SegDesc*>(dv),
+                  reinterpret_cast<const PairDesc*>(dv + pair_off),
+                  static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),
+                  static_cast<uint32_t>(cpt));
+  if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
+  return ring_commit(ctx->ring, off, total, stream);
+}
+
+int aegkv_host_alloc(void** ptr, int64_t bytes) {
+  g_err[0] = '\0';
+  if (!ptr || bytes <= 0) return fail(AEGKV_EINVAL, "host_alloc needs a pointer and bytes > 0");
+  void* p = nullptr;
+  AEGKV_HIP(hipHostMalloc(&p, static_cast<size_t>(bytes),
+                          hipHostMallocMapped | hipHostMallocPortable));
+  {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    g_host_allocs[reinterpret_cast<uintptr_t>(p)] = static_cast<size_t>(bytes);
+  }
+  *ptr = p;
+  return 0;
+}
+
+int aegkv_host_free(void* ptr) {
+  g_err[0] = '\0';
+  if (!ptr) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    g_host_allocs.erase(reinterpret_cast<uintptr_t>(ptr));
+  }
+  AEGKV_HIP(hipHostFree(ptr));
+  return 0;
+}
+
+}  // extern "C"

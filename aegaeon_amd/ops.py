@@ -1,0 +1,281 @@
+"""Operator API of the KV movement path (the `aegaeon.ops` drop-in).
+
+`swap` keeps the reference's positional signature, ops/ops.h:4-10
+(`swap(source_block_ids, target_block_ids, is_swap_in, kv_cache, kv_swap)`),
+and runs on the current stream like ops/swap.cu:21-32. `swap_segments` is the
+composite-page data plane of Worker.swap_blocks (aegaeon/worker.py:2265-2329)
+and `copy_blocks` the in-HBM block copy. Every call is one C-ABI call into
+libaegkv.so; there is no Python or CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+
+MODE_AUTO = _lib.MODE_AUTO
+MODE_DIRECT = _lib.MODE_DIRECT
+MODE_STAGED = _lib.MODE_STAGED
+
+_MODES = {"auto": MODE_AUTO, "direct": MODE_DIRECT, "staged": MODE_STAGED}
+
+
+def _mode(mode) -> int:
+    if isinstance(mode, str):
+        try:
+            return _MODES[mode]
+        except KeyError:
+            raise ValueError(f"unknown transfer mode {mode!r}") from None
+    if mode not in (MODE_AUTO, MODE_DIRECT, MODE_STAGED):
+        raise ValueError(f"unknown transfer mode {mode!r}")
+    return int(mode)
+
+
+def _i64(values) -> np.ndarray:
+    if isinstance(values, torch.Tensor):
+        values = values.detach().cpu().numpy()
+    a = np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+    return a
+
+
+def _i32(values) -> np.ndarray:
+    if isinstance(values, torch.Tensor):
+        values = values.detach().cpu().numpy()
+    return np.ascontiguousarray(np.asarray(values, dtype=np.int32).reshape(-1))
+
+
+def _p64(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))
+
+
+def _p32(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def _pu64(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64))
+
+
+def _stream_ptr(device: torch.device, stream: torch.cuda.Stream | None) -> int:
+    s = stream if stream is not None else torch.cuda.current_stream(device)
+    return s.cuda_stream
+
+
+def _tensor_bytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def _require_device(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise ValueError(f"{what} must be a device (HIP) tensor, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+def _require_host(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cpu":
+        raise ValueError(f"{what} must be a host tensor, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+
+
+def swap(
+    source_block_ids: Sequence[int],
+    target_block_ids: Sequence[int],
+    is_swap_in: bool,
+    kv_cache: torch.Tensor,
+    kv_swap: torch.Tensor,
+    *,
+    mode="auto",
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """Whole-block swap between a device cache and a pinned host pool.
+
+    Follows ops/swap.cu:25-60: block i moves source_block_ids[i] ->
+    target_block_ids[i]; is_swap_in copies host (kv_swap) -> device
+    (kv_cache), otherwise device -> host. The block size is
+    kv_cache.numel() * element_size / kv_cache.size(0) bytes and is used for
+    both tensors; for the 2-byte dtypes the reference supports this equals
+    its `numel * 2 / size(0)` (swap.cu:34). Runs on the current stream.
+    Raises ValueError on bad ids (the reference checks nothing).
+    """
+    _require_device(kv_cache, "kv_cache")
+    _require_host(kv_swap, "kv_swap")
+    src = _i64(source_block_ids)
+    dst = _i64(target_block_ids)
+    if src.shape != dst.shape:
+        raise ValueError(
+            f"source ({src.size}) and target ({dst.size}) id lists differ in length"
+        )
+    if kv_cache.dim() == 0 or kv_cache.size(0) == 0:
+        raise ValueError("kv_cache must have a non-empty block dimension")
+    block_bytes = _tensor_bytes(kv_cache) // kv_cache.size(0)
+    if _tensor_bytes(kv_cache) % kv_cache.size(0):
+        raise ValueError("kv_cache bytes are not divisible by its block count")
+    swap_blocks_total = _tensor_bytes(kv_swap) // block_bytes
+    lib = _lib.load()
+    with torch.cuda.device(kv_cache.device):
+        rc = lib.aegkv_swap(
+            _p64(src), _p64(dst), src.size, 1 if is_swap_in else 0,
+            kv_cache.data_ptr(), kv_cache.size(0),
+            kv_swap.data_ptr(), swap_blocks_total, block_bytes,
+            _mode(mode), _stream_ptr(kv_cache.device, stream),
+        )
+    _lib.check(rc)
+
+
+def swap_segments(
+    segments: Sequence[torch.Tensor],
+    segment_page_bytes: Sequence[int],
+    segment_host_offsets: Sequence[int],
+    segment_owner_masks: Sequence[int],
+    device_num_blocks: int,
+    group_kernel_blocks_per_page: Sequence[int],
+    host_pool: torch.Tensor,
+    host_page_bytes: int,
+    host_rank_offset: int,
+    source_block_ids,
+    target_block_ids,
+    group_ids,
+    first_kernel_blocks,
+    valid_kernel_blocks,
+    is_swap_in: bool,
+    *,
+    mode="auto",
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """Composite-page swap of (segment x entry) extents in one launch.
+
+    Byte placement of aegaeon/worker.py:2265-2329: for each segment s owned
+    by the entry's group, extent (off, len) = byte_extent_for_kernel_blocks
+    of (page_s, kernel blocks per page, first, valid) (cache_transfer.py:
+    138-165); host bytes sit at host_id * host_page_bytes + host_rank_offset
+    + host_offset_s + off; device bytes at dev_id * page_s + off of segment s.
+    """
+    if not segments:
+        raise ValueError("at least one segment is required")
+    dev = segments[0].device
+    for i, t in enumerate(segments):
+        _require_device(t, f"segment {i}")
+        if t.device != dev:
+            raise ValueError("all segments must live on one device")
+    _require_host(host_pool, "host_pool")
+    n_seg = len(segments)
+    page = _i64(segment_page_bytes)
+    hoff = _i64(segment_host_offsets)
+    owners = np.ascontiguousarray(np.asarray(segment_owner_masks, dtype=np.uint64).reshape(-1))
+    kpp = _i64(group_kernel_blocks_per_page)
+    if not (page.size == hoff.size == owners.size == n_seg):
+        raise ValueError("segment metadata lengths must equal the number of segments")
+    for i, t in enumerate(segments):
+        if _tensor_bytes(t) < int(page[i]) * device_num_blocks:
+            raise ValueError(
+                f"segment {i} holds {_tensor_bytes(t)} bytes < {device_num_blocks} x {int(page[i])}"
+            )
+    src = _i64(source_block_ids)
+    dst = _i64(target_block_ids)
+    grp = _i32(group_ids)
+    first = _i64(first_kernel_blocks)
+    valid = _i64(valid_kernel_blocks)
+    lengths = {src.size, dst.size, grp.size, first.size, valid.size}
+    if len(lengths) != 1:
+        raise ValueError(
+            "Swap block ids and metadata must have equal lengths: "
+            f"source={src.size}, target={dst.size}, groups={grp.size}, "
+            f"first={first.size}, valid={valid.size}"
+        )
+    bases = (ctypes.c_void_p * n_seg)(*[t.data_ptr() for t in segments])
+    host_blocks = _tensor_bytes(host_pool) // host_page_bytes if host_page_bytes > 0 else 0
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.aegkv_swap_blocks(
+            n_seg, bases, _p64(page), _p64(hoff), _pu64(owners), int(device_num_blocks),
+            kpp.size, _p64(kpp), host_pool.data_ptr(), host_blocks, int(host_page_bytes),
+            int(host_rank_offset), src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
+            _p64(valid), 1 if is_swap_in else 0, _mode(mode), _stream_ptr(dev, stream),
+        )
+    _lib.check(rc)
+
+
+def copy_blocks(
+    segments: Sequence[torch.Tensor],
+    src_block_ids,
+    dst_block_ids,
+    *,
+    segment_page_bytes: Sequence[int] | None = None,
+    device_num_blocks: int | None = None,
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """In-HBM block copy: seg[dst[i]] := seg[src[i]] for every segment.
+
+    Each segment is viewed as [num_blocks, page] bytes; by default the page
+    is the tensor's bytes / size(0). Targets must be distinct and disjoint
+    from the sources. The reference has no KV copy_blocks; its in-HBM
+    compaction is aegaeon/allocator.py:101-137.
+    """
+    if not segments:
+        raise ValueError("at least one segment is required")
+    dev = segments[0].device
+    for i, t in enumerate(segments):
+        _require_device(t, f"segment {i}")
+        if t.device != dev:
+            raise ValueError("all segments must live on one device")
+    if device_num_blocks is None:
+        device_num_blocks = segments[0].size(0)
+    if segment_page_bytes is None:
+        segment_page_bytes = [_tensor_bytes(t) // device_num_blocks for t in segments]
+    page = _i64(segment_page_bytes)
+    if page.size != len(segments):
+        raise ValueError("segment_page_bytes must have one entry per segment")
+    for i, t in enumerate(segments):
+        if _tensor_bytes(t) < int(page[i]) * device_num_blocks:
+            raise ValueError(f"segment {i} is smaller than {device_num_blocks} blocks")
+    src = _i64(src_block_ids)
+    dst = _i64(dst_block_ids)
+    if src.shape != dst.shape:
+        raise ValueError("src and dst id lists differ in length")
+    bases = (ctypes.c_void_p * len(segments))(*[t.data_ptr() for t in segments])
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.aegkv_copy_blocks(
+            len(segments), bases, _p64(page), int(device_num_blocks), src.size, _p64(src),
+            _p64(dst), _stream_ptr(dev, stream),
+        )
+    _lib.check(rc)
+
+
+class PinnedHostPool:
+    """A pinned, device-mapped host byte pool from aegkv_host_alloc.
+
+    Counterpart of the reference's host KV pool (aegaeon/llm.py:1020-1040,
+    aegaeon/worker.py:251-273), allocated pinned instead of registering an
+    existing /dev/shm mapping. `tensor` is a uint8 view of the whole pool.
+    """
+
+    def __init__(self, nbytes: int):
+        if nbytes <= 0:
+            raise ValueError("pool size must be positive")
+        lib = _lib.load()
+        ptr = ctypes.c_void_p()
+        _lib.check(lib.aegkv_host_alloc(ctypes.byref(ptr), int(nbytes)))
+        self._ptr = ptr.value
+        self.nbytes = int(nbytes)
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(self._ptr)
+        self.tensor = torch.frombuffer(buf, dtype=torch.uint8)
+
+    def free(self) -> None:
+        if self._ptr:
+            self.tensor = None
+            _lib.check(_lib.load().aegkv_host_free(self._ptr))
+            self._ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -1,0 +1,156 @@
+/*
+ * aegkv.h - C ABI of libaegkv.so, the MI355X (gfx950) KV-cache movement
+ * library: paged K/V block swap-out (HBM -> pinned host), swap-in
+ * (pinned host -> HBM) and in-HBM block copy.
+ *
+ * Conventions shared by every entry point
+ *   - Plain pointers and sizes only. Device pointers are HIP device
+ *     addresses on the *current* HIP device; host pool pointers must come
+ *     from hipHostMalloc (aegkv_host_alloc or a pinned torch tensor).
+ *   - Id arrays and metadata arrays are HOST arrays, read during the call.
+ *     The library validates them completely before enqueueing anything,
+ *     then uploads a compact descriptor through its own stream-ordered
+ *     pinned->device ring, so the caller may reuse the arrays on return.
+ *   - All work is enqueued on `stream` (a hipStream_t; torch's
+ *     torch.cuda.current_stream().cuda_stream). Nothing synchronises the
+ *     host except when the upload ring is full and must wait for an older
+ *     call on some stream to retire.
+ *   - Return value: 0 on success; a negative AEGKV_E* code for an invalid
+ *     argument (nothing was enqueued); a positive hipError_t value when the
+ *     HIP runtime failed. aegkv_last_error() gives a message for the
+ *     calling thread's most recent failure.
+ *   - The caller keeps every buffer alive until the stream has passed the
+ *     enqueued work (record an event after the call and wait on it).
+ */
+#ifndef AEGKV_H
+#define AEGKV_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AEGKV_ABI_VERSION 1
+
+/* status codes (negative: rejected before any work was enqueued) */
+#define AEGKV_OK 0
+#define AEGKV_EINVAL (-1)        /* malformed argument (null, negative size) */
+#define AEGKV_ERANGE (-2)        /* block id / group id outside its pool     */
+#define AEGKV_EDUP (-3)          /* a target block id appears twice          */
+#define AEGKV_EEXTENT (-4)       /* kernel-block extent outside the page     */
+#define AEGKV_EOVERLAP (-5)      /* copy_blocks: a source is also a target   */
+#define AEGKV_ENOMEM (-6)        /* descriptor larger than the upload ring   */
+
+/* host-transfer designs for swap-out / swap-in */
+#define AEGKV_MODE_AUTO 0   /* library choice (per direction, measured)        */
+#define AEGKV_MODE_DIRECT 1 /* gather/scatter kernel reads/writes the pinned
+                               host pool directly over PCIe                    */
+#define AEGKV_MODE_STAGED 2 /* gather/scatter kernel <-> contiguous device
+                               staging, plus SDMA hipMemcpyAsync of merged runs */
+
+/* tuning keys for aegkv_tune (values < 0 query without changing) */
+#define AEGKV_TUNE_WGS_PER_CU 1      /* persistent workgroups per CU      */
+#define AEGKV_TUNE_STAGING_BYTES 2   /* max device staging per chunk      */
+#define AEGKV_TUNE_AUTO_D2H 3        /* mode AUTO picks for swap-out      */
+#define AEGKV_TUNE_AUTO_H2D 4        /* mode AUTO picks for swap-in       */
+#define AEGKV_TUNE_NT_STORES 5       /* 1: non-temporal stores in copies  */
+
+/* ABI version of the loaded library (AEGKV_ABI_VERSION). */
+int aegkv_abi_version(void);
+
+/* Message for the calling thread's most recent failure ("" if none). */
+const char* aegkv_last_error(void);
+
+/* Set a tuning knob; returns the previous value (or <0 on a bad key). */
+int64_t aegkv_tune(int key, int64_t value);
+
+/*
+ * Legacy whole-block swap. Replaces ops/ops.h:4-10 / ops/swap.cu:25-60
+ * (`swap(source_block_ids, target_block_ids, is_swap_in, kv_cache,
+ * kv_swap)`): for i < num_ids, with B = block_bytes,
+ *   is_swap_in:  kv_cache[target[i]*B ..+B) <- kv_swap[source[i]*B ..+B)
+ *   otherwise:   kv_swap[target[i]*B ..+B)  <- kv_cache[source[i]*B ..+B)
+ * kv_cache is device memory of cache_num_blocks blocks, kv_swap a pinned
+ * host pool of swap_num_blocks blocks. Unlike the reference (which checks
+ * nothing and assumes 2-byte elements when deriving B, swap.cu:34), ids are
+ * range-checked and duplicate targets are rejected; the caller passes B.
+ */
+int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
+               int64_t num_ids, int is_swap_in,
+               void* kv_cache, int64_t cache_num_blocks,
+               void* kv_swap, int64_t swap_num_blocks,
+               int64_t block_bytes, int mode, hipStream_t stream);
+
+/*
+ * Segmented (composite-page) swap. Replaces the data-plane loop of
+ * Worker.swap_blocks, aegaeon/worker.py:2265-2329, whose layout comes from
+ * aegaeon/vllm_cache.py:75-101 and aegaeon/worker.py:1419-1432.
+ *
+ * Layout: segment s is one backing tensor viewed as
+ * [device_num_blocks, segment_page_bytes[s]] bytes at segment_bases[s].
+ * A host block id owns host_page_bytes bytes of host_pool (the composite
+ * page times the tensor-parallel size); this rank's composite page starts
+ * at host_rank_offset inside it and segment s sits at
+ * segment_host_offsets[s] inside that.
+ *
+ * Entry e = (source_block_ids[e], target_block_ids[e], group_ids[e],
+ * first_kernel_blocks[e], valid_kernel_blocks[e]). For every segment s
+ * owned by group g = group_ids[e] (bit g of segment_owner_masks[s]):
+ *   unit = segment_page_bytes[s] / group_kernel_blocks_per_page[g]
+ *   off  = unit * first, len = unit * valid   (cache_transfer.py:138-165)
+ *   host = host_pool + host_id*host_page_bytes + host_rank_offset
+ *          + segment_host_offsets[s] + off
+ *   dev  = segment_bases[s] + dev_id*segment_page_bytes[s] + off
+ *   is_swap_in: dev[0,len) <- host[0,len)  (host_id = source, dev_id = target)
+ *   otherwise:  host[0,len) <- dev[0,len)  (dev_id = source, host_id = target)
+ * Entries with len == 0 and segments not owned by g move nothing.
+ */
+int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
+                      const int64_t* segment_page_bytes,
+                      const int64_t* segment_host_offsets,
+                      const uint64_t* segment_owner_masks,
+                      int64_t device_num_blocks,
+                      int32_t num_groups,
+                      const int64_t* group_kernel_blocks_per_page,
+                      void* host_pool, int64_t host_num_blocks,
+                      int64_t host_page_bytes, int64_t host_rank_offset,
+                      int64_t num_entries,
+                      const int64_t* source_block_ids,
+                      const int64_t* target_block_ids,
+                      const int32_t* group_ids,
+                      const int64_t* first_kernel_blocks,
+                      const int64_t* valid_kernel_blocks,
+                      int is_swap_in, int mode, hipStream_t stream);
+
+/*
+ * In-HBM block copy / compaction: for every segment s and pair i,
+ *   seg_s[dst[i]] := seg_s[src[i]]   (one whole block of segment_page_bytes[s]).
+ * The reference has no KV copy_blocks (block_manager.py:1392-1393); its
+ * in-HBM compactions are aegaeon/allocator.py:101-137 (relocate_tensors),
+ * aegaeon/graph_bindings.py:60-92 and aegaeon/loader/allocator.py:288-321.
+ * Targets must be distinct and disjoint from the sources (AEGKV_EDUP /
+ * AEGKV_EOVERLAP otherwise), which makes the result independent of order.
+ */
+int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
+                      const int64_t* segment_page_bytes,
+                      int64_t device_num_blocks, int64_t num_pairs,
+                      const int64_t* src_block_ids,
+                      const int64_t* dst_block_ids, hipStream_t stream);
+
+/*
+ * Pinned host pool. Replaces the pinning half of the reference's host KV
+ * pool set-up: Controller._init_cpu_cache (aegaeon/llm.py:1020-1040) and
+ * the worker's cudaHostRegister of that mapping (aegaeon/worker.py:251-273).
+ * Allocates with hipHostMalloc (mapped + portable, so kernels on every
+ * device may access it). The pool is not zero-filled.
+ */
+int aegkv_host_alloc(void** ptr, int64_t bytes);
+int aegkv_host_free(void* ptr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AEGKV_H */
