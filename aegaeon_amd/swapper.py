@@ -1,0 +1,160 @@
+"""Worker-side swap execution: the data plane of Worker.swap_blocks.
+
+Mirrors aegaeon/worker.py: the segment -> owning-group map (:1397-1417),
+the host page view (:1419-1432), the swap streams (:278-280),
+swap_blocks (:2204-2349), the source-event waits (:2351-2394) and
+wait_for_all_move_in/out (:2406-2418). The reference issues one
+torch copy_ per (segment, entry) extent from a Python double loop; here the
+whole list is one call into libaegkv.so, one kernel launch per call.
+
+Cross-process plumbing (Ray object refs, CUDA IPC event handles) is not part
+of this module: source events are local torch.cuda.Event objects and the
+returned completion event is a local event.
+"""
+
+from __future__ import annotations
+
+import logging
+from collections import defaultdict
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import ops
+from .cache_groups import CacheGroupRuntimeConfig
+from .layout import CompositeCache, host_page_geometry
+
+logger = logging.getLogger("aegaeon_amd.swap")
+
+
+class KVSwapper:
+    """Executes swap lists between a CompositeCache and a pinned host pool."""
+
+    def __init__(self, cache: CompositeCache, group_layer_names: Sequence[set],
+                 group_descriptors: Sequence[CacheGroupRuntimeConfig],
+                 host_pool: torch.Tensor, tp_rank: int = 0, tp_size: int = 1,
+                 host_element_size: int = 2):
+        if len(group_layer_names) != len(group_descriptors):
+            raise ValueError("one layer-name set per cache group is required")
+        if len(group_descriptors) > 64:
+            raise ValueError("at most 64 cache groups are supported")
+        if not 0 <= tp_rank < tp_size:
+            raise ValueError(f"tp_rank {tp_rank} outside [0, {tp_size})")
+        self.cache = cache
+        self.group_descriptors = list(group_descriptors)
+        self.tp_rank = tp_rank
+        self.tp_size = tp_size
+        # segment -> owning groups (worker.py:1403-1417)
+        self.segment_group_ids: List[frozenset] = []
+        for seg in cache.segments:
+            owners = frozenset(g for g, names in enumerate(group_layer_names)
+                               if set(seg.shared_by) & set(names))
+            if not owners:
+                raise ValueError(f"Cache segment {seg.layer_name} is not owned by any "
+                                 "KV-cache group")
+            self.segment_group_ids.append(owners)
+        # host view (worker.py:1419-1432)
+        self.host_page_bytes = host_page_geometry(cache.page_size_bytes, tp_size,
+                                                  host_element_size)
+        if host_pool.dtype != torch.uint8:
+            host_pool = host_pool.view(torch.uint8)
+        self.num_host_blocks = host_pool.numel() // self.host_page_bytes
+        self.kv_swap_view = host_pool.narrow(
+            0, 0, self.num_host_blocks * self.host_page_bytes
+        ).view(self.num_host_blocks, self.host_page_bytes)
+        # flattened C-ABI layout
+        self._segments = [cache.segment_tensor(i) for i in range(len(cache.segments))]
+        self._page = np.array([s.page_size_bytes for s in cache.segments], np.int64)
+        self._cpu_off = np.array([s.cpu_offset for s in cache.segments], np.int64)
+        self._owner_mask = np.array(
+            [sum(1 << g for g in owners) for owners in self.segment_group_ids], np.uint64)
+        self._kpp = np.array([d.blocks_per_kv_block for d in self.group_descriptors], np.int64)
+        for s, owners in enumerate(self.segment_group_ids):
+            for g in owners:
+                if self._page[s] % self._kpp[g]:
+                    raise ValueError(
+                        f"Backing page size {int(self._page[s])} is not divisible by "
+                        f"{int(self._kpp[g])} kernel blocks"
+                    )
+        # bytes and extents one entry of group g moves per kernel block
+        n_groups = len(self.group_descriptors)
+        self._bytes_per_kb = np.zeros(n_groups, np.int64)
+        self._extents_per_entry = np.zeros(n_groups, np.int64)
+        for s, owners in enumerate(self.segment_group_ids):
+            for g in owners:
+                self._bytes_per_kb[g] += self._page[s] // self._kpp[g]
+                self._extents_per_entry[g] += 1
+        device = self._segments[0].device
+        self.device = device
+        self.swap_in_stream = torch.cuda.Stream(device)
+        self.swap_out_stream = torch.cuda.Stream(device)
+        self.move_event_table: Dict[int, List[torch.cuda.Event]] = defaultdict(list)
+
+    def swap_blocks(self, request_ids: Sequence[int], source_block_ids: Sequence[int],
+                    target_block_ids: Sequence[int], group_ids: Sequence[int],
+                    first_kernel_blocks: Sequence[int], valid_kernel_blocks: Sequence[int],
+                    source_events: Sequence[Optional[torch.cuda.Event]], is_swap_in: bool,
+                    mode="auto") -> torch.cuda.Event:
+        """Move the live extents of some blocks between host and device.
+
+        is_swap_in: host block source_block_ids[i] -> device block
+        target_block_ids[i]; otherwise device -> host. Waits on the source
+        events of requests that still have a move in flight, then enqueues
+        the whole list on the swap stream and returns an event recorded
+        behind it (worker.py:2204-2349).
+        """
+        lengths = {len(source_block_ids), len(target_block_ids), len(group_ids),
+                   len(first_kernel_blocks), len(valid_kernel_blocks)}
+        if len(lengths) != 1:
+            raise ValueError(
+                "Swap block ids and metadata must have equal lengths: "
+                f"source={len(source_block_ids)}, target={len(target_block_ids)}, "
+                f"groups={len(group_ids)}, first={len(first_kernel_blocks)}, "
+                f"valid={len(valid_kernel_blocks)}"
+            )
+        groups = np.asarray(group_ids, dtype=np.int64).reshape(-1)
+        if groups.size and (groups.min() < 0 or groups.max() >= len(self.group_descriptors)):
+            bad = groups[(groups < 0) | (groups >= len(self.group_descriptors))][0]
+            raise ValueError(f"Invalid swap cache-group id {int(bad)}")
+        if len(source_events) != len(request_ids):
+            raise ValueError("one source event slot per request is required")
+        stream = self.swap_in_stream if is_swap_in else self.swap_out_stream
+        new_event = torch.cuda.Event()
+        # wait for in-flight moves of the same requests (worker.py:2351-2394)
+        for rid, ev in zip(request_ids, source_events):
+            if ev is not None:
+                stream.wait_event(ev)
+            self.move_event_table[rid].append(new_event)
+        ops.swap_segments(
+            self._segments, self._page, self._cpu_off, self._owner_mask,
+            self.cache.num_blocks, self._kpp, self.kv_swap_view.view(-1),
+            self.host_page_bytes, self.tp_rank * self.cache.page_size_bytes,
+            source_block_ids, target_block_ids, groups.astype(np.int32),
+            first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode, stream=stream,
+        )
+        new_event.record(stream)
+        if logger.isEnabledFor(logging.INFO):
+            valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
+            copied = int((valid * self._bytes_per_kb[groups]).sum()) if groups.size else 0
+            extents = int(((valid > 0) * self._extents_per_entry[groups]).sum()) if groups.size else 0
+            full = len(source_block_ids) * self.cache.page_size_bytes
+            saved = 0.0 if full == 0 else 1.0 - copied / full
+            logger.info("swap requests %s (%s to %s): copied %d/%d bytes (saved %.2f%%), "
+                        "%d extents in one launch", list(request_ids),
+                        "CPU" if is_swap_in else "GPU", "GPU" if is_swap_in else "CPU",
+                        copied, full, saved * 100, extents)
+        return new_event
+
+    def clear_request_resource(self, request_id: int) -> None:
+        self.move_event_table.pop(request_id, None)
+
+    def clear_request_resource_batched(self, request_ids: Sequence[int]) -> None:
+        for rid in request_ids:
+            self.clear_request_resource(rid)
+
+    def wait_for_all_move_in(self) -> None:
+        self.swap_in_stream.synchronize()
+
+    def wait_for_all_move_out(self) -> None:
+        self.swap_out_stream.synchronize()

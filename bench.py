@@ -1,0 +1,333 @@
+#!/usr/bin/env python
+"""Benchmark of the KV-cache movement path on one MI355X.
+
+Metric: KV swap GB/s (D2H/H2D, % of the measured host link) + HBM
+block-copy GB/s (% of HBM peak). GB = 1e9 bytes.
+
+One step = one pass of the path over one batch:
+  * Qwen3-4B KV shape (72 x [8192,16,8,128] bf16): swap-out of 1024 seeded
+    non-contiguous device blocks to a 4096-block pinned host pool, then
+    swap-in of those 1024 host blocks to 1024 fresh device ids;
+  * Llama-2-13B KV shape (80 x [8192,16,40,128] fp16): copy_blocks of 4096
+    (src, dst) pairs, distinct targets disjoint from the sources.
+Every operation is one libaegkv call on the current stream, timed with HIP
+events recorded on that stream. `value` is the swap throughput (both
+directions' bytes over their summed time); the copy_blocks kernel carries
+the HBM roofline, the swaps the measured-host-link roofline.
+
+The CPU baseline times the reference's torch path (one narrow().copy_() per
+(segment, block) extent, aegaeon/worker.py:2272-2328) on host tensors of the
+Qwen3-4B shape with 2048 blocks: gather 256 blocks into contiguous staging,
+scatter them to 256 other ids.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = ("KV swap GB/s (D2H/H2D, % host link) + HBM block-copy GB/s (% HBM peak)")
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+TRAFFIC_FILE = REPO / "profiles" / "copy_blocks_traffic.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-runs", type=int, default=5)
+    return p.parse_args()
+
+
+def kv_segments(torch, n_layers, n_blocks, heads, dim, dtype, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    segs = []
+    for _ in range(2 * n_layers):
+        t = torch.empty(n_blocks, 16, heads, dim, dtype=dtype, device=dev)
+        t.normal_(generator=g)
+        segs.append(t)
+    return segs
+
+
+def measure_link(torch, ops, dev, nbytes=1 << 30, reps=3):
+    """Host-link ceilings: contiguous pinned hipMemcpyAsync each way, best of reps."""
+    pool = ops.PinnedHostPool(nbytes)
+    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    out = {}
+    for name, fn in (("d2h", lambda: pool.tensor.copy_(d, non_blocking=True)),
+                     ("h2d", lambda: d.copy_(pool.tensor, non_blocking=True))):
+        best = 0.0
+        for _ in range(reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            best = max(best, nbytes / (a.elapsed_time(b) / 1e3) / 1e9)
+        out[name] = best
+    del d
+    pool.free()
+    return out
+
+
+def measure_stream_copy(torch, dev, nbytes=4 << 30, reps=3):
+    """Plain device-to-device copy of known size (torch's copy kernel)."""
+    a_ = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b_ = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    best = 0.0
+    for _ in range(reps + 1):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        b_.copy_(a_)
+        e1.record()
+        e1.synchronize()
+        best = max(best, 2 * nbytes / (e0.elapsed_time(e1) / 1e3) / 1e9)
+    del a_, b_
+    return best
+
+
+def cpu_baseline(runs: int):
+    """The reference's torch path on host tensors (oracle restatement)."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle
+
+    layers, blocks, heads, dim = 36, 2048, 8, 128
+    g = torch.Generator().manual_seed(0)
+    tensors = [torch.randn(blocks, 16, heads, dim, generator=g).to(torch.bfloat16)
+               for _ in range(2 * layers)]
+    pages = [t.view(torch.uint8).view(blocks, -1) for t in tensors]
+    tile = pages[0].shape[1]
+    S = len(pages)
+    composite = S * tile
+    n = 256
+    perm = torch.randperm(blocks - 1, generator=g) + 1
+    src, dst = perm[:n].tolist(), perm[n:2 * n].tolist()
+    staging = torch.empty(n, composite, dtype=torch.uint8)
+    owners = [{0}] * S
+    cpu_off = [s * tile for s in range(S)]
+    z, one = [0] * n, [1] * n
+    threads = torch.get_num_threads()
+    torch.set_num_threads(1)  # the timed loop: one thread (extents sit at torch's grain size)
+    times = []
+    for r in range(runs + 1):
+        t0 = time.perf_counter()
+        oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite, src,
+                                 list(range(n)), z, z, one, False)
+        oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite,
+                                 list(range(n)), dst, z, z, one, True)
+        dt = time.perf_counter() - t0
+        if r:
+            times.append(dt)
+    idx_s, idx_d = torch.tensor(src), torch.tensor(dst)
+    ok = all(torch.equal(p[idx_d], p[idx_s]) for p in pages)
+    if not ok:
+        raise AssertionError("CPU baseline round trip is not bit-exact")
+    torch.set_num_threads(threads)
+    t = statistics.median(times)
+    moved = 2 * n * composite
+    return {
+        "value": round(moved / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"reference torch path (per-extent narrow().copy_(), worker.py:2272-2328) on "
+                   f"host tensors: 72 x [2048,16,8,128] bf16 N(0,1); gather 256 blocks to "
+                   f"staging + scatter to 256 other ids = {moved} bytes; median of {runs} runs, "
+                   f"torch threads 1 of os.cpu_count()={os.cpu_count()}; bit-exact round trip"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "
+              "(swaps shard per GPU with no exchange step; run one process per GPU).",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+
+    log("measuring host-link and stream-copy ceilings")
+    link = measure_link(torch, ops, dev)
+    stream_copy = measure_stream_copy(torch, dev)
+
+    # ---- Qwen3-4B swap workload
+    log("allocating Qwen3-4B KV cache and pinned pool")
+    L1, NB1, H1, D1, HOST1, NSW = 36, 8192, 8, 128, 4096, 1024
+    segs1 = kv_segments(torch, L1, NB1, H1, D1, torch.bfloat16, dev, 1)
+    S1 = len(segs1)
+    tile1 = 16 * H1 * D1 * 2
+    pool = ops.PinnedHostPool(HOST1 * S1 * tile1)
+    g = torch.Generator().manual_seed(1)
+    out_ids = (torch.randperm(NB1 - 1, generator=g)[:NSW] + 1).numpy()
+    host_ids = torch.randperm(HOST1, generator=g)[:NSW].numpy()
+    rest = np.setdiff1d(np.arange(1, NB1), out_ids)
+    in_ids = rest[torch.randperm(rest.size, generator=g)[:NSW].numpy()]
+    common1 = ([tile1] * S1, [s * tile1 for s in range(S1)], [1] * S1, NB1, [1], pool.tensor,
+               S1 * tile1, 0)
+    zero = np.zeros(NSW, np.int32)
+    ones = np.ones(NSW, np.int64)
+    swap_bytes = NSW * S1 * tile1
+
+    # ---- Llama-2-13B copy_blocks workload
+    log("allocating Llama-2-13B KV cache")
+    L2, NB2, H2, D2, NP = 40, 8192, 40, 128, 4096
+    segs2 = kv_segments(torch, L2, NB2, H2, D2, torch.float16, dev, 2)
+    S2 = len(segs2)
+    tile2 = 16 * H2 * D2 * 2
+    g2 = torch.Generator().manual_seed(2)
+    perm = torch.randperm(NB2, generator=g2)
+    csrc, cdst = perm[:NP].numpy(), perm[NP:2 * NP].numpy()
+    copy_bytes = 2 * NP * S2 * tile2
+
+    def step(evs):
+        evs[0].record()
+        ops.swap_segments(segs1, *common1, out_ids, host_ids, zero, zero, ones, False,
+                          mode=args.mode)
+        evs[1].record()
+        ops.swap_segments(segs1, *common1, host_ids, in_ids, zero, zero, ones, True,
+                          mode=args.mode)
+        evs[2].record()
+        ops.copy_blocks(segs2, csrc, cdst)
+        evs[3].record()
+
+    def events():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        step(events())
+    torch.cuda.synchronize()
+
+    log(f"timing {args.steps} steps")
+    all_evs = [events() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for evs in all_evs:
+        step(evs)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    d2h = [e[0].elapsed_time(e[1]) / 1e3 for e in all_evs]
+    h2d = [e[1].elapsed_time(e[2]) / 1e3 for e in all_evs]
+    cpy = [e[2].elapsed_time(e[3]) / 1e3 for e in all_evs]
+
+    # ---- correctness of what was timed (size-independent properties)
+    di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
+    swap_ok = all(torch.equal(s[di], s[do]) for s in segs1)
+    cs, cd = torch.from_numpy(csrc).to(dev), torch.from_numpy(cdst).to(dev)
+    copy_ok = all(torch.equal(s[cd], s[cs]) for s in segs2)
+    if not (swap_ok and copy_ok):
+        raise AssertionError(f"bit-exact check failed: swap {swap_ok}, copy_blocks {copy_ok}")
+
+    t_d2h, t_h2d, t_cpy = sum(d2h) / len(d2h), sum(h2d) / len(h2d), sum(cpy) / len(cpy)
+    d2h_gbps = swap_bytes / t_d2h / 1e9
+    h2d_gbps = swap_bytes / t_h2d / 1e9
+    swap_gbps = 2 * swap_bytes / (t_d2h + t_h2d) / 1e9
+    copy_gbps = copy_bytes / t_cpy / 1e9
+    resolved = {0: "direct", 1: "direct", 2: "staged"}
+    mode_d2h = args.mode if args.mode != "auto" else resolved[_lib.tune(_lib.TUNE_AUTO_D2H)]
+    mode_h2d = args.mode if args.mode != "auto" else resolved[_lib.tune(_lib.TUNE_AUTO_H2D)]
+
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        tr = json.loads(TRAFFIC_FILE.read_text())
+        if tr.get("workload") == "llama2-13b copy_blocks 4096 pairs":
+            traffic = tr.get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(swap_gbps, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic: seeded N(0,1) bf16/fp16 KV caches, seeded block ids",
+        "config": {
+            "workload": ("Qwen3-4B KV swap-out + swap-in of 1024 blocks (72 x [8192,16,8,128] "
+                         "bf16, 4096-block pinned pool) + Llama-2-13B copy_blocks of 4096 pairs "
+                         "(80 x [8192,16,40,128] fp16)"),
+            "swap_bytes_per_direction": swap_bytes,
+            "copy_blocks_bytes_rw": copy_bytes,
+            "transfer_mode": {"d2h": mode_d2h, "h2d": mode_h2d},
+        },
+        "swap": {
+            "d2h_GBps": round(d2h_gbps, 3),
+            "h2d_GBps": round(h2d_gbps, 3),
+            "d2h_blocks_per_s": round(NSW / t_d2h, 1),
+            "h2d_blocks_per_s": round(NSW / t_h2d, 1),
+            "link_d2h_GBps": round(link["d2h"], 3),
+            "link_h2d_GBps": round(link["h2d"], 3),
+            "d2h_frac_link": round(d2h_gbps / link["d2h"], 4),
+            "h2d_frac_link": round(h2d_gbps / link["h2d"], 4),
+        },
+        "copy_blocks": {
+            "GBps_rw": round(copy_gbps, 1),
+            "pairs_per_s": round(NP / t_cpy, 1),
+            "frac_hbm_peak": round(copy_gbps / HBM_PEAK_GBPS, 4),
+            "stream_copy_ceiling_GBps": round(stream_copy, 1),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "copy_blocks_kernel",
+            "achieved": round(copy_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(copy_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "avg_launch_ms": round(t_cpy * 1e3, 3),
+        },
+        "link_roofline": {
+            "bound": "host-link (measured)",
+            "kernel": "swap_tiles_kernel",
+            "achieved_d2h": round(d2h_gbps, 3),
+            "achieved_h2d": round(h2d_gbps, 3),
+            "peak_d2h": round(link["d2h"], 3),
+            "peak_h2d": round(link["h2d"], 3),
+            "unit": "GB/s",
+            "frac_d2h": round(d2h_gbps / link["d2h"], 4),
+            "frac_h2d": round(h2d_gbps / link["h2d"], 4),
+            "avg_launch_ms_d2h": round(t_d2h * 1e3, 3),
+            "avg_launch_ms_h2d": round(t_h2d * 1e3, 3),
+        },
+    }
+    pool.free()
+    del segs1, segs2
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (reference torch path on host tensors)")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_runs)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

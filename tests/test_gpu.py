@@ -1,0 +1,361 @@
+"""GPU parity: libaegkv kernels against the oracle and the golden fixtures.
+
+Every comparison is byte equality. Small cases compare with the oracle run
+on host copies of the same seeded inputs; full-size cases (the benchmark
+shapes) check size-independent properties: swap-out/swap-in round trips,
+host pages equal to the device tiles they came from, untouched blocks
+unchanged.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from aegaeon_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+MODES = ("direct", "staged")
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _pool_from(arr: np.ndarray) -> ops.PinnedHostPool:
+    pool = ops.PinnedHostPool(arr.size)
+    pool.tensor.copy_(torch.from_numpy(arr.reshape(-1)))
+    return pool
+
+
+# ------------------------------------------------------------ golden cases --
+
+@pytest.mark.parametrize("mode", MODES)
+def test_legacy_swap_golden(gpu, golden, mode):
+    z = golden("legacy_swap.npz")
+    shape = tuple(int(x) for x in z["cache_shape"])
+    cache = torch.from_numpy(z["cache"].copy()).view(torch.bfloat16).view(shape).to(gpu)
+    pool = torch.from_numpy(z["pool"].copy()).view(torch.bfloat16).view(
+        (z["pool"].shape[0],) + shape[1:]).pin_memory()
+    ops.swap(z["out_src"].tolist(), z["out_dst"].tolist(), False, cache, pool, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.view(torch.uint8).reshape(pool.shape[0], -1).numpy(),
+                          z["pool_after_out"])
+    ops.swap(z["in_src"].tolist(), z["in_dst"].tolist(), True, cache, pool, mode=mode)
+    torch.cuda.synchronize()
+    got = cache.cpu().view(torch.uint8).reshape(shape[0], -1).numpy()
+    assert np.array_equal(got, z["cache_after_in"])
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_composite_swap_golden(gpu, golden, mode):
+    z = golden("composite_swap.npz")
+    segs = [torch.from_numpy(z[f"seg{s}"].copy()).to(gpu) for s in range(5)]
+    pool = _pool_from(z["host"])
+    common = (z["page"], z["cpu_off"], z["owners"], int(z["n_gpu"]), z["kpp"], pool.tensor,
+              int(z["host_page"]), int(z["tp_rank"]) * int(z["composite"]))
+    ops.swap_segments(segs, *common, z["src"], z["dst"], z["grp"], z["first"], z["valid"],
+                      False, mode=mode)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.tensor.numpy().reshape(z["host"].shape), z["host_after_out"])
+    ops.swap_segments(segs, *common, z["in_src"], z["in_dst"], z["grp"], z["first"],
+                      z["valid"], True, mode=mode)
+    torch.cuda.synchronize()
+    for s in range(5):
+        assert np.array_equal(segs[s].cpu().numpy(), z[f"seg{s}_after_in"]), s
+    pool.free()
+
+
+def test_copy_blocks_golden(gpu, golden):
+    z = golden("copy_blocks.npz")
+    segs = [torch.from_numpy(z[f"seg{i}"].copy()).to(gpu) for i in range(3)]
+    ops.copy_blocks(segs, z["src"], z["dst"])
+    torch.cuda.synchronize()
+    for i in range(3):
+        assert np.array_equal(segs[i].cpu().numpy(), z[f"seg{i}_after"])
+
+
+# ------------------------------------------------------- seeded vs oracle --
+
+def _random_layout(rng):
+    """Mixed page sizes (16 B multiples up to 80 KiB), 3 groups, TP 2."""
+    n_groups = 3
+    kpp = np.array([1, 4, 2], np.int64)
+    n_seg = 11
+    page = (rng.integers(1, 5, n_seg) * 4 * 16 * rng.choice([1, 16, 80, 320], n_seg)).astype(np.int64)
+    owners = rng.integers(1, 1 << n_groups, n_seg).astype(np.uint64)
+    cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)
+    return kpp, page, owners, cpu_off
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("mode", MODES)
+def test_seeded_swap_vs_oracle(gpu, oracle, seed, mode):
+    rng = np.random.default_rng(100 + seed)
+    kpp, page, owners, cpu_off = _random_layout(rng)
+    composite = int(page.sum())
+    tp_size, tp_rank = 2, seed % 2
+    host_page = composite * tp_size
+    n_gpu, n_host, n = 48, 40, 30
+    _say("seeded swap", seed, mode, "segments", len(page), "composite", composite)
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    host_np = rng.integers(0, 256, (n_host, host_page), dtype=np.uint8)
+    grp = rng.integers(0, 3, n).astype(np.int32)
+    first = np.array([rng.integers(0, kpp[g] + 1) for g in grp], np.int64)
+    valid = np.array([rng.integers(0, kpp[g] - f + 1) for g, f in zip(grp, first)], np.int64)
+    src = rng.permutation(n_gpu)[:n]
+    dst = rng.permutation(n_host)[:n]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    pool = _pool_from(host_np)
+    common = (page, cpu_off, owners, n_gpu, kpp, pool.tensor, host_page, tp_rank * composite)
+    ops.swap_segments(segs, *common, src, dst, grp, first, valid, False, mode=mode)
+    want_host = host_np.copy()
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       want_host.reshape(-1), host_page, tp_rank, composite, src, dst, grp,
+                       first, valid, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.tensor.numpy().reshape(want_host.shape), want_host)
+    # swap back in to other device ids
+    back = rng.permutation(n_gpu)[:n]
+    ops.swap_segments(segs, *common, dst, back, grp, first, valid, True, mode=mode)
+    want_segs = [x.copy() for x in segs_np]
+    oracle.swap_blocks([x.reshape(-1) for x in want_segs], page, cpu_off, owners, n_gpu, kpp,
+                       want_host.reshape(-1), host_page, tp_rank, composite, dst, back, grp,
+                       first, valid, True)
+    torch.cuda.synchronize()
+    for s in range(len(page)):
+        assert np.array_equal(segs[s].cpu().numpy(), want_segs[s]), s
+    pool.free()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_unaligned_host_pool_vs_oracle(gpu, oracle, mode):
+    """A host pool starting 1 byte into its allocation forces the
+    byte-granular kernel path (and unaligned DMA in staged mode)."""
+    rng = np.random.default_rng(7)
+    page = np.array([256, 512, 64], np.int64)
+    cpu_off = np.array([0, 256, 768], np.int64)
+    owners = np.ones(3, np.uint64)
+    kpp = np.array([4], np.int64)
+    composite = 832
+    n_gpu, n_host, n = 16, 12, 9
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    raw = ops.PinnedHostPool(n_host * composite + 1)
+    raw.tensor.zero_()
+    host = raw.tensor.narrow(0, 1, n_host * composite)
+    src, dst = rng.permutation(n_gpu)[:n], rng.permutation(n_host)[:n]
+    first = rng.integers(0, 3, n)
+    valid = np.array([rng.integers(0, 4 - f + 1) for f in first])
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    ops.swap_segments(segs, page, cpu_off, owners, n_gpu, kpp, host, composite, 0, src, dst,
+                      np.zeros(n, np.int32), first, valid, False, mode=mode)
+    want = np.zeros((n_host, composite), np.uint8)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       want.reshape(-1), composite, 0, composite, src, dst,
+                       np.zeros(n, np.int32), first, valid, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(host.numpy().reshape(want.shape), want)
+    assert raw.tensor[0].item() == 0
+    raw.free()
+
+
+def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
+    rng = np.random.default_rng(3)
+    n = 64
+    page = np.array([16, 4096, 160 * 1024, 48 * 1024 + 16, 100], np.int64)  # last: byte path
+    segs_np = [rng.integers(0, 256, (n, int(p)), dtype=np.uint8) for p in page]
+    perm = rng.permutation(n)
+    src, dst = perm[:25], perm[25:50]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np[:4]]
+    ops.copy_blocks(segs, src, dst)
+    oracle.copy_blocks([x.reshape(-1) for x in segs_np[:4]], page[:4], n, src, dst)
+    torch.cuda.synchronize()
+    for s in range(4):
+        assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), s
+    # unaligned page size takes the byte path
+    seg = torch.from_numpy(segs_np[4].copy()).to(gpu)
+    ops.copy_blocks([seg], src, dst)
+    oracle.copy_blocks([segs_np[4].reshape(-1)], page[4:], n, src, dst)
+    torch.cuda.synchronize()
+    assert np.array_equal(seg.cpu().numpy(), segs_np[4])
+
+
+# --------------------------------------------------------- error behaviour --
+
+def test_rejections_enqueue_nothing(gpu):
+    seg = torch.arange(8 * 64, dtype=torch.int32, device=gpu).view(torch.uint8).view(8, 256)
+    before = seg.clone()
+    pool = ops.PinnedHostPool(4 * 256)
+    pool.tensor.fill_(7)
+    args = ([256], [0], [1], 8, [1], pool.tensor, 256, 0)
+    cases = [
+        ([1, 2], [0, 4], "target"),     # host id 4 outside [0, 4)
+        ([9], [0], "source"),           # device id 9 outside [0, 8)
+        ([1, 2], [3, 3], "twice"),      # duplicate target
+    ]
+    for src, dst, word in cases:
+        with pytest.raises(ValueError, match=word):
+            ops.swap_segments([seg], *args, src, dst, [0] * len(src), [0] * len(src),
+                              [1] * len(src), False)
+    with pytest.raises(ValueError, match="exceeds"):
+        ops.swap_segments([seg], *args, [1], [0], [0], [0], [2], False)
+    with pytest.raises(ValueError, match="equal lengths"):
+        ops.swap_segments([seg], *args, [1], [0], [0, 0], [0], [1], False)
+    with pytest.raises(ValueError, match="both a source and a target"):
+        ops.copy_blocks([seg], [1, 2], [2, 3])
+    with pytest.raises(ValueError, match="twice"):
+        ops.copy_blocks([seg], [1, 2], [3, 3])
+    pageable = torch.zeros(4 * 256, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="pinned"):
+        ops.swap_segments([seg], [256], [0], [1], 8, [1], pageable, 256, 0, [1], [0], [0],
+                          [0], [1], False, mode="direct")
+    torch.cuda.synchronize()
+    assert torch.equal(seg, before)
+    assert bool((pool.tensor == 7).all())
+    pool.free()
+
+
+def test_runs_on_current_stream_and_orders_by_events(gpu):
+    """Work goes on the caller's current stream (ops/swap.cu:21-32): a
+    consumer on another stream sees the data only after waiting on an event
+    recorded behind the swap."""
+    n, page = 64, 65536
+    seg = torch.randint(0, 256, (n, page), dtype=torch.uint8, device=gpu)
+    pool = ops.PinnedHostPool(n * page)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        ops.swap_segments([seg], [page], [0], [1], n, [1], pool.tensor, page, 0,
+                          np.arange(n), np.arange(n)[::-1].copy(), np.zeros(n, np.int32),
+                          np.zeros(n), np.ones(n), False)
+        done = torch.cuda.Event()
+        done.record(side)
+    fresh = torch.zeros_like(seg)
+    torch.cuda.current_stream().wait_event(done)
+    ops.swap_segments([fresh], [page], [0], [1], n, [1], pool.tensor, page, 0,
+                      np.arange(n)[::-1].copy(), np.arange(n), np.zeros(n, np.int32),
+                      np.zeros(n), np.ones(n), True)
+    torch.cuda.synchronize()
+    assert torch.equal(fresh, seg)
+    pool.free()
+
+
+# ------------------------------------------------------------ swapper --
+
+def test_swapper_block_table_round_trip(gpu, oracle):
+    """BlockTable.transfer_entries -> KVSwapper.swap_blocks out and back in,
+    partial extents included, checked against the oracle."""
+    from aegaeon_amd.cache_groups import BlockTable, CacheGroupConfig, CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import KVSwapper
+
+    n_blocks, n_host = 40, 32
+    specs = [KVCacheTensorSpec(n_blocks * 4096, ("full.0",)),
+             KVCacheTensorSpec(n_blocks * 4096, ("win.0",)),
+             KVCacheTensorSpec(n_blocks * 8192, ("full.1", "win.1"))]
+    cache = allocate_composite_cache(specs, n_blocks, gpu)
+    for t in cache.backing:
+        t.random_(-128, 127)
+    groups = (CacheGroupConfig("attention", 64, 16), CacheGroupConfig("attention", 64, 16, 40))
+    descr = [CacheGroupRuntimeConfig("attention", 64, 16),
+             CacheGroupRuntimeConfig("attention", 64, 16, 40)]
+    pool = ops.PinnedHostPool(n_host * cache.page_size_bytes)
+    pool.tensor.zero_()
+    sw = KVSwapper(cache, [{"full.0", "full.1"}, {"win.0", "win.1"}], descr, pool.tensor)
+    table = BlockTable(0, (cache.page_size_bytes // 2,), groups,
+                       [[3, 4, 5, 6], [7, 8, 9, 10]])
+    tokens = 230
+    rows = table.transfer_entries(tokens)
+    copy = [r for r in rows if r[4] > 0]
+    host_ids = list(range(len(copy)))
+    dev_src = [r[2] for r in copy]
+    before = [t.cpu().numpy().view(np.uint8).copy() for t in cache.backing]
+    ev = sw.swap_blocks([1], dev_src, host_ids, [r[0] for r in copy], [r[3] for r in copy],
+                        [r[4] for r in copy], [None], False)
+    ev.synchronize()
+    owners = np.array([1, 2, 3], np.uint64)
+    page = np.array([4096, 4096, 8192], np.int64)
+    want_host = np.zeros((n_host, cache.page_size_bytes), np.uint8)
+    oracle.swap_blocks([x.reshape(-1) for x in before], page, [0, 4096, 8192], owners,
+                       n_blocks, [4, 4], want_host.reshape(-1), cache.page_size_bytes, 0,
+                       cache.page_size_bytes, dev_src, host_ids, [r[0] for r in copy],
+                       [r[3] for r in copy], [r[4] for r in copy], False)
+    assert np.array_equal(pool.tensor.numpy().reshape(want_host.shape), want_host)
+    new_ids = [20 + i for i in range(len(copy))]
+    ev2 = sw.swap_blocks([1], host_ids, new_ids, [r[0] for r in copy], [r[3] for r in copy],
+                         [r[4] for r in copy], [ev], True)
+    sw.wait_for_all_move_in()
+    oracle.swap_blocks([x.reshape(-1) for x in before], page, [0, 4096, 8192], owners,
+                       n_blocks, [4, 4], want_host.reshape(-1), cache.page_size_bytes, 0,
+                       cache.page_size_bytes, host_ids, new_ids, [r[0] for r in copy],
+                       [r[3] for r in copy], [r[4] for r in copy], True)
+    for t, w in zip(cache.backing, before):
+        assert np.array_equal(t.cpu().numpy().view(np.uint8), w)
+    assert ev2.query()
+    pool.free()
+
+
+# ---------------------------------------------------- full benchmark shapes --
+
+def _kv_segments(n_layers, n_blocks, heads, dim, dtype, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    segs = []
+    for _ in range(2 * n_layers):
+        t = torch.empty(n_blocks, 16, heads, dim, dtype=dtype, device=dev)
+        t.normal_(generator=g)
+        segs.append(t)
+    return segs
+
+
+def test_qwen3_4b_swap_full_size_round_trip(gpu):
+    """72 x [8192,16,8,128] bf16; 1024 non-contiguous blocks out to a 4096
+    block pinned pool and back in to fresh ids; host pages must equal the
+    device tiles they came from and the round trip must be exact."""
+    _say("Qwen3-4B full-size round trip")
+    segs = _kv_segments(36, 8192, 8, 128, torch.bfloat16, gpu, 1)
+    tile = 16 * 8 * 128 * 2
+    S = len(segs)
+    pool = ops.PinnedHostPool(4096 * S * tile)
+    g = torch.Generator().manual_seed(1)
+    out_ids = (torch.randperm(8191, generator=g)[:1024] + 1).numpy()
+    host_ids = torch.randperm(4096, generator=g)[:1024].numpy()
+    rest = np.setdiff1d(np.arange(1, 8192), out_ids)
+    in_ids = rest[torch.randperm(rest.size, generator=g)[:1024].numpy()]
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, 8192, [1], pool.tensor,
+              S * tile, 0)
+    z = np.zeros(1024, np.int32)
+    for mode in MODES:
+        ops.swap_segments(segs, *common, out_ids, host_ids, z, z, z + 1, False, mode=mode)
+        ops.swap_segments(segs, *common, host_ids, in_ids, z, z, z + 1, True, mode=mode)
+        torch.cuda.synchronize()
+        dev_in = torch.from_numpy(in_ids).to(gpu)
+        dev_out = torch.from_numpy(out_ids).to(gpu)
+        for s in range(S):
+            assert torch.equal(segs[s][dev_in], segs[s][dev_out]), (mode, s)
+        pages = pool.tensor.view(4096, S, tile)
+        for k in (0, 511, 1023):
+            for s in (0, 37, 71):
+                assert torch.equal(pages[int(host_ids[k]), s].to(gpu),
+                                   segs[s][int(out_ids[k])].view(torch.uint8).reshape(-1))
+    pool.free()
+
+
+def test_llama2_13b_copy_blocks_full_size(gpu):
+    """80 x [8192,16,40,128] fp16 (100 GiB); 4096 pairs, distinct targets
+    disjoint from the sources: every target equals its source afterwards and
+    every other block keeps its checksum."""
+    _say("Llama-2-13B full-size copy_blocks")
+    segs = _kv_segments(40, 8192, 40, 128, torch.float16, gpu, 2)
+    g = torch.Generator().manual_seed(2)
+    perm = torch.randperm(8192, generator=g)
+    src, dst = perm[:4096], perm[4096:]
+    keep = torch.ones(8192, dtype=torch.bool)
+    keep[dst] = False
+    keep = keep.to(gpu)
+    sums = [s.view(8192, -1).view(torch.int16).sum(dim=1, dtype=torch.int64) for s in segs]
+    ops.copy_blocks(segs, src.numpy(), dst.numpy())
+    torch.cuda.synchronize()
+    ds, dd = src.to(gpu), dst.to(gpu)
+    for i, s in enumerate(segs):
+        assert torch.equal(s[dd], s[ds]), i
+        after = s.view(8192, -1).view(torch.int16).sum(dim=1, dtype=torch.int64)
+        assert torch.equal(after[keep], sums[i][keep]), i

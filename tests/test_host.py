@@ -1,0 +1,252 @@
+"""Host-side logic and the C-ABI library, without a GPU."""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from aegaeon_amd import cache_transfer as ct
+from aegaeon_amd.cache_groups import (
+    LOGICAL_NULL_BLOCK_ID,
+    BlockTable,
+    CacheGroupConfig,
+    CacheGroupRuntimeConfig,
+)
+from aegaeon_amd.layout import KVCacheTensorSpec, kv_tensor_specs, make_composite_layout
+
+REPO = Path(__file__).resolve().parent.parent
+
+
+# ------------------------------------------------------------ cache_transfer --
+
+def test_product_extent_matches_oracle(oracle, golden):
+    rows = golden("kernel_block_extent.npz")["rows"]
+    for t, b, phys, kern, w, f, c in rows.tolist():
+        w = None if w < 0 else w
+        assert ct.kernel_block_extent_for_attention_page(t, b, phys, kern, w) == (f, c)
+    for page, kpp in ((2162688, 33), (384, 4), (65536, 1)):
+        for first in range(kpp + 1):
+            for num in range(kpp - first + 1):
+                assert ct.byte_extent_for_kernel_blocks(page, kpp, first, num) == \
+                    oracle.byte_extent(page, kpp, first, num)
+
+
+@pytest.mark.parametrize("args", [
+    (-1, 0, 16, 16, None), (0, -1, 16, 16, None), (0, 0, 0, 16, None), (0, 0, 16, 0, None),
+    (0, 0, 48, 32, None), (5, 0, 16, 16, 0),
+])
+def test_product_extent_rejects_like_oracle(oracle, args):
+    with pytest.raises(ValueError):
+        oracle.kernel_block_extent(*args)
+    with pytest.raises(ValueError):
+        ct.kernel_block_extent_for_attention_page(*args)
+
+
+def test_product_window_helpers_match_oracle(oracle):
+    for bs in (1, 4, 16):
+        for w in (1, 2, 5, 16, 33):
+            for t in range(0, 80):
+                assert ct.logical_blocks_for_tokens(t, bs) == oracle.logical_blocks_for_tokens(t, bs)
+                assert ct.num_skipped_sliding_window_blocks(t, bs, w) == \
+                    oracle.num_skipped_sliding_window_blocks(t, bs, w)
+                assert ct.sliding_window_resident_block_bound(t, bs, w) == \
+                    oracle.sliding_window_resident_block_bound(t, bs, w)
+                assert ct.valid_kernel_blocks_for_attention_page(t, 1, 32, bs) == \
+                    oracle.kernel_block_extent(t, 1, 32, bs)[1] if 32 % bs == 0 else True
+    for bad in ((-1, 16), (3, 0)):
+        with pytest.raises(ValueError):
+            ct.logical_blocks_for_tokens(*bad)
+    with pytest.raises(ValueError):
+        ct.prefix_bytes_for_kernel_blocks(384, 4, 5)
+    with pytest.raises(ValueError):
+        ct.byte_extent_for_kernel_blocks(384, 4, 3, 2)
+
+
+# ------------------------------------------------------------ cache groups --
+
+def test_to_kernel_block_ids_known_answer():
+    """block_manager.py:342-344: 272-token physical / 16-token kernel blocks,
+    physical id 3 -> kernel ids 51..67; a released column -> the null block."""
+    g = CacheGroupRuntimeConfig("attention", 272, 16)
+    assert g.to_kernel_block_ids([3]) == list(range(51, 68))
+    assert g.to_kernel_block_ids([-1]) == [0] * 17
+    assert CacheGroupRuntimeConfig("mamba_none", 4, 4).to_kernel_block_ids([5, 9]) == [5, 9]
+
+
+def test_slot_for_position():
+    g = CacheGroupRuntimeConfig("attention", 64, 16)
+    ids = [7, -1, 2]
+    # position 130 -> column 2 (id 2), inside 2 -> kernel id 2*4 + 0 -> slot 8*16 + 2
+    assert g.slot_for_position(ids, 130) == 130 - 128 + 2 * 64
+    assert g.slot_for_position(ids, 17) == 7 * 64 + 17
+    with pytest.raises(RuntimeError):
+        g.slot_for_position(ids, 70)
+    with pytest.raises(IndexError):
+        g.slot_for_position(ids, 200)
+
+
+def test_group_validation():
+    with pytest.raises(ValueError):
+        CacheGroupConfig("attention", 48, 32)
+    with pytest.raises(ValueError):
+        CacheGroupConfig("mamba_none", 16, 8)
+    with pytest.raises(ValueError):
+        CacheGroupConfig("mamba_none", 16, 16, sliding_window=4)
+    with pytest.raises(ValueError):
+        CacheGroupConfig("attention", 16, 16, sliding_window=0)
+    with pytest.raises(NotImplementedError):
+        CacheGroupConfig("linear", 16, 16)
+
+
+def _table():
+    groups = (CacheGroupConfig("attention", 32, 16),
+              CacheGroupConfig("attention", 32, 16, sliding_window=20),
+              CacheGroupConfig("mamba_none", 1, 1))
+    return BlockTable(location=0, block_shape=(8,), cache_groups=groups,
+                      group_blocks=[[5, 6, 7, 8], [9, 10, 11, 12], [13]])
+
+
+def test_transfer_entries_brute_force(oracle):
+    """Every retained page, with its live kernel-block extent; pages wholly
+    before the window are skipped; the mamba page moves whole."""
+    t = 100
+    rows = _table().transfer_entries(t)
+    want = []
+    for col in range(4):
+        want.append((0, col, 5 + col) + oracle.kernel_block_extent(t, col, 32, 16))
+    skipped = max(0, t - 20 + 1) // 32
+    for col in range(skipped, 4):
+        want.append((1, col, 9 + col) + oracle.kernel_block_extent(t, col, 32, 16, 20))
+    want.append((2, 0, 13, 0, 1))
+    assert rows == want
+    assert skipped == 2
+
+
+def test_moved_tables_and_metadata():
+    tab = _table()
+    t = 100
+    rows = tab.transfer_entries(t)
+    targets = list(range(100, 100 + len(rows)))
+    moved = tab.moved_group_blocks(t, targets)
+    assert moved[1][:2] == [LOGICAL_NULL_BLOCK_ID] * 2
+    flat = [b for col in moved for b in col if b != LOGICAL_NULL_BLOCK_ID]
+    assert flat == targets
+    with pytest.raises(ValueError):
+        tab.moved_group_blocks(t, targets[:-1])
+    groups, firsts, counts = tab.swap_metadata(t)
+    assert all(c > 0 for c in counts)
+    assert len(groups) == sum(1 for r in rows if r[4] > 0)
+
+
+def test_release_and_replace():
+    tab = _table()
+    released = tab.release_skipped_blocks(100)
+    assert released == [9, 10]
+    assert tab.group_blocks[1][:2] == [LOGICAL_NULL_BLOCK_ID] * 2
+    assert tab.blocks == [5, 6, 7, 8, 11, 12, 13]
+    tab.replace_flat_blocks([1, 2, 3, 4, 5, 6, 7])
+    assert tab.group_blocks == [[1, 2, 3, 4], [-1, -1, 5, 6], [7]]
+    with pytest.raises(ValueError):
+        tab.replace_flat_blocks([1])
+
+
+def test_sliding_window_one_keeps_destination_without_bytes():
+    """A W=1 window retains its current page with nothing to copy
+    (block_manager.py:1440-1446): count 0, still a transfer entry."""
+    groups = (CacheGroupConfig("attention", 16, 16, sliding_window=1),)
+    tab = BlockTable(0, (8,), groups, [[4, 5]])
+    rows = tab.transfer_entries(20)
+    assert rows == [(0, 1, 5, 0, 0)]
+    assert tab.swap_metadata(20) == ([], [], [])
+
+
+# ------------------------------------------------------------------ layout --
+
+def test_composite_layout():
+    specs = kv_tensor_specs(36, 8, 16, 8, 128, 2)
+    segs, page = make_composite_layout(specs, 8)
+    assert len(segs) == 72
+    assert page == 72 * 32768 == 2_359_296
+    assert [s.cpu_offset for s in segs[:3]] == [0, 32768, 65536]
+    assert segs[1].layer_name == "layers.0.v"
+    with pytest.raises(ValueError):
+        make_composite_layout([KVCacheTensorSpec(10, ("a",))], 3)
+    with pytest.raises(NotImplementedError):
+        make_composite_layout([KVCacheTensorSpec(12, ("a",), block_stride=4)], 3)
+    with pytest.raises(ValueError):
+        make_composite_layout([KVCacheTensorSpec(12, ())], 3)
+
+
+# ------------------------------------------------------------------ C ABI --
+
+def _declared_symbols():
+    hdr = (REPO / "include" / "aegkv.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(aegkv_\w+)\(", hdr, re.M)))
+
+
+def test_library_exports_every_declared_symbol(aegkv_lib):
+    from aegaeon_amd import _lib
+
+    declared = _declared_symbols()
+    assert declared == sorted(_lib.EXPORTED_SYMBOLS)
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (aegkv_\w+)", out))
+    for name in declared:
+        assert name in exported, name
+        assert hasattr(aegkv_lib, name)
+    assert aegkv_lib.aegkv_abi_version() == _lib.ABI_VERSION
+
+
+def test_library_binds_to_torch_hip_runtime():
+    """Every HIP symbol libaegkv imports must be exported by the HIP runtime
+    torch ships, so that in a torch process both share one runtime."""
+    import torch
+    from aegaeon_amd import _lib
+
+    torch_hip = Path(torch.__file__).parent / "lib" / "libamdhip64.so"
+    if not torch_hip.exists():
+        pytest.skip("torch without a bundled HIP runtime")
+    need = subprocess.run(["nm", "-D", "--undefined-only", str(_lib.LIB_PATH)],
+                          capture_output=True, text=True, check=True).stdout
+    have = subprocess.run(["nm", "-D", "--defined-only", str(torch_hip)],
+                          capture_output=True, text=True, check=True).stdout
+    have_syms = set(re.findall(r" [TW] (\S+)", have))
+    for sym in re.findall(r" U (\S*hip\S*)", need):
+        assert sym.replace("@", "@@", 1) in have_syms or sym.split("@")[0] in have_syms, sym
+
+
+def test_early_validation_without_gpu(aegkv_lib):
+    from aegaeon_amd import _lib
+
+    lib = aegkv_lib
+    rc = lib.aegkv_swap(None, None, 0, 0, None, 1, None, 1, 0, 0, None)
+    assert rc == _lib.EINVAL
+    assert b"block_bytes" in lib.aegkv_last_error()
+    rc = lib.aegkv_copy_blocks(0, None, None, 1, 0, None, None, None)
+    assert rc == _lib.EINVAL
+    rc = lib.aegkv_swap_blocks(1, None, None, None, None, 1, 1, None, None, 1, 1, 0, 1, None,
+                               None, None, None, None, 0, 0, None)
+    assert rc == _lib.EINVAL
+    assert b"metadata" in lib.aegkv_last_error()
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+    assert lib.aegkv_host_alloc(None, 16) == _lib.EINVAL
+    assert lib.aegkv_host_free(None) == 0
+
+
+def test_tuning_knobs(aegkv_lib):
+    from aegaeon_amd import _lib
+
+    prev = _lib.tune(_lib.TUNE_WGS_PER_CU)
+    assert prev >= 1
+    assert _lib.tune(_lib.TUNE_WGS_PER_CU, 4) == prev
+    assert _lib.tune(_lib.TUNE_WGS_PER_CU, prev) == 4
+    assert _lib.tune(_lib.TUNE_AUTO_D2H) in (_lib.MODE_DIRECT, _lib.MODE_STAGED)
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_AUTO_D2H, 7)
+    with pytest.raises(ValueError):
+        _lib.tune(99, 1)
