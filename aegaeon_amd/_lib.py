@@ -36,6 +36,9 @@ TUNE_STAGING_BYTES = 2
 TUNE_AUTO_D2H = 3
 TUNE_AUTO_H2D = 4
 TUNE_NT_STORES = 5
+TUNE_COPY_WGS_PER_CU = 6
+TUNE_COPY_UNROLL = 7
+TUNE_SWAP_SHAPE_AUTO = 8
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (

@@ -63,11 +63,14 @@ int hip_fail(hipError_t e, const char* what) {
 // --------------------------------------------------------------- tunables --
 
 struct Tunables {
-  int64_t wgs_per_cu = 8;
+  int64_t wgs_per_cu = 8;        // swap kernels: persistent workgroups per CU
   int64_t staging_bytes = int64_t(512) << 20;
   int64_t auto_d2h = AEGKV_MODE_DIRECT;
   int64_t auto_h2d = AEGKV_MODE_DIRECT;
   int64_t nt_stores = 1;
+  int64_t copy_wgs_per_cu = 0;   // copy_blocks: 0 = one workgroup per work item
+  int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
+  int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
 };
 Tunables g_tune;
 std::mutex g_tune_mu;
@@ -78,10 +81,6 @@ Tunables tunables() {
 }
 
 // ------------------------------------------------------ device descriptors --
-
-constexpr int kWG = 256;    // lanes per workgroup (4 wavefronts of 64)
-constexpr int kUnroll = 4;  // 16 B loads in flight per lane per item
-constexpr int64_t kChunk = int64_t(kWG) * 16 * kUnroll;  // 16 KiB per item
 
 struct SegDesc {            // one backing tensor
   char* base;
@@ -110,36 +109,45 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) v4u gv4u;  // global (VM) address space
 typedef __attribute__((address_space(1))) char gchar;
 
-// Move nbytes (multiple of 16, at most kChunk) with 16 B per lane. A full
-// chunk issues all kUnroll loads back to back before any store; only a
-// tail chunk pays for per-load guards.
-template <bool NT_STORE>
+// A kernel "shape": WG lanes per workgroup, U 16-byte loads in flight per
+// lane, so one work item (chunk) is WG * 16 * U bytes.
+template <int WG, int U>
+struct Shape {
+  static constexpr int kLanes = WG;
+  static constexpr int kLoads = U;
+  static constexpr int64_t kChunk = int64_t(WG) * 16 * U;
+};
+
+// Move nbytes (multiple of 16, at most one chunk) with 16 B per lane. A full
+// chunk issues all U loads back to back before the first store; only a tail
+// chunk pays for per-load guards.
+template <int WG, int U, bool NT_STORE>
 __device__ __forceinline__ void move_chunk16(const char* src, char* dst, uint32_t nbytes) {
   const gv4u* s = (const gv4u*)src;  // generic -> global address space
   gv4u* d = (gv4u*)dst;
   const uint32_t tid = threadIdx.x;
-  v4u r[kUnroll];
-  if (nbytes == static_cast<uint32_t>(kChunk)) {
+  v4u r[U];
+  if (nbytes == static_cast<uint32_t>(Shape<WG, U>::kChunk)) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) r[u] = __builtin_nontemporal_load(s + tid + u * kWG);
+    for (int u = 0; u < U; ++u) r[u] = __builtin_nontemporal_load(s + tid + u * WG);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
       if (NT_STORE)
-        __builtin_nontemporal_store(r[u], d + tid + u * kWG);
+        __builtin_nontemporal_store(r[u], d + tid + u * WG);
       else
-        d[tid + u * kWG] = r[u];
+        d[tid + u * WG] = r[u];
     }
     return;
   }
   const uint32_t n16 = nbytes >> 4;
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const uint32_t i = tid + u * kWG;
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tid + u * WG;
     if (i < n16) r[u] = __builtin_nontemporal_load(s + i);
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const uint32_t i = tid + u * kWG;
+  for (int u = 0; u < U; ++u) {
+    const uint32_t i = tid + u * WG;
     if (i < n16) {
       if (NT_STORE)
         __builtin_nontemporal_store(r[u], d + i);
@@ -150,20 +158,22 @@ __device__ __forceinline__ void move_chunk16(const char* src, char* dst, uint32_
 }
 
 // Byte-granular fallback for callers whose offsets are not 16 B aligned.
+template <int WG>
 __device__ __forceinline__ void move_chunk_bytes(const char* src, char* dst, uint32_t nbytes) {
   const gchar* s = (const gchar*)src;
   gchar* d = (gchar*)dst;
-  for (uint32_t i = threadIdx.x; i < nbytes; i += kWG) d[i] = s[i];
+  for (uint32_t i = threadIdx.x; i < nbytes; i += WG) d[i] = s[i];
 }
 
 // Swap tile mover. Item w -> (entry e, segment s, chunk c), entry-major.
 // TO_HOST: device tile -> host side; otherwise host side -> device tile.
 // The host checks num_items < 2^32 so item decoding stays 32-bit.
-template <bool TO_HOST, bool VEC, bool NT_STORE>
-__global__ __launch_bounds__(kWG) void swap_tiles_kernel(
+template <int WG, int U, bool TO_HOST, bool VEC, bool NT_STORE>
+__global__ __launch_bounds__(WG) void swap_tiles_kernel(
     const SegDesc* __restrict__ segs, const EntDesc* __restrict__ ents,
     const int64_t* __restrict__ kpp, uint32_t num_segs, uint32_t num_items,
     uint32_t chunks_per_tile, char* host_base, int64_t host_stride, int64_t host_rank_offset) {
+  constexpr int64_t kChunk = Shape<WG, U>::kChunk;
   for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
     const uint32_t tile = w / chunks_per_tile;
     const uint32_t c = w - tile * chunks_per_tile;
@@ -184,17 +194,18 @@ __global__ __launch_bounds__(kWG) void swap_tiles_kernel(
     const char* src = TO_HOST ? dev : host;
     char* dst = TO_HOST ? host : dev;
     if (VEC)
-      move_chunk16<NT_STORE>(src, dst, nbytes);
+      move_chunk16<WG, U, NT_STORE>(src, dst, nbytes);
     else
-      move_chunk_bytes(src, dst, nbytes);
+      move_chunk_bytes<WG>(src, dst, nbytes);
   }
 }
 
 // copy_blocks: item w -> (pair p, segment s, chunk c), pair-major.
-template <bool VEC, bool NT_STORE>
-__global__ __launch_bounds__(kWG) void copy_blocks_kernel(
+template <int WG, int U, bool VEC, bool NT_STORE>
+__global__ __launch_bounds__(WG) void copy_blocks_kernel(
     const SegDesc* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
     uint32_t num_items, uint32_t chunks_per_tile) {
+  constexpr int64_t kChunk = Shape<WG, U>::kChunk;
   for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
     const uint32_t tile = w / chunks_per_tile;
     const uint32_t c = w - tile * chunks_per_tile;
@@ -209,10 +220,37 @@ __global__ __launch_bounds__(kWG) void copy_blocks_kernel(
     const char* src = seg.base + pr.src * seg.page_bytes + begin;
     char* dst = seg.base + pr.dst * seg.page_bytes + begin;
     if (VEC)
-      move_chunk16<NT_STORE>(src, dst, nbytes);
+      move_chunk16<WG, U, NT_STORE>(src, dst, nbytes);
     else
-      move_chunk_bytes(src, dst, nbytes);
+      move_chunk_bytes<WG>(src, dst, nbytes);
   }
+}
+
+// Shapes the library instantiates. 1024-lane shapes move 16 KiB rows; a
+// tile that is a multiple of 16 KiB gets the largest U dividing its row
+// count, so one workgroup moves a whole tile (up to 160 KiB) with no tail
+// chunk. Smaller tiles use 256-lane (4 KiB) rows.
+struct ShapeSel {
+  int wg;
+  int u;
+  int64_t chunk() const { return int64_t(wg) * 16 * u; }
+};
+
+ShapeSel auto_shape(int64_t page) {
+  static const int kBigU[] = {10, 8, 6, 5, 4, 3, 2, 1};
+  const int64_t row = 1024 * 16;
+  if (page >= row && page % row == 0) {
+    const int64_t rows = page / row;
+    for (int u : kBigU)
+      if (rows % u == 0) return {1024, u};
+  }
+  if (page >= row) return {1024, 4};
+  const int64_t small_rows = (page + 4095) / 4096;
+  return {256, small_rows <= 1 ? 1 : (small_rows <= 2 ? 2 : 4)};
+}
+
+bool valid_copy_unroll(int64_t u) {
+  return u == 1 || u == 2 || u == 3 || u == 4 || u == 5 || u == 6 || u == 8 || u == 10;
 }
 
 // ------------------------------------------------------- per-device state --
@@ -398,53 +436,80 @@ int check_host_range(const void* ptr, int64_t bytes, const char* what) {
 
 // ----------------------------------------------------------- launching --
 
-int64_t grid_for(const DeviceCtx* ctx, int64_t items) {
-  const Tunables t = tunables();
-  int64_t g = static_cast<int64_t>(ctx->num_cus) * std::max<int64_t>(1, t.wgs_per_cu);
-  return std::max<int64_t>(1, std::min<int64_t>(g, items));
+// Workgroups to launch: wgs_per_cu per CU striding over the items, or one
+// per item when wgs_per_cu is 0. An HSA dispatch counts work-items in 32
+// bits, so the grid is capped at (2^32 - 1) / lanes; the kernels' grid-stride
+// loops cover any remainder.
+int64_t launch_grid(const DeviceCtx* ctx, int64_t wgs_per_cu, int64_t items, int lanes) {
+  const int64_t cap = static_cast<int64_t>(UINT32_MAX) / lanes;
+  int64_t g = items;
+  if (wgs_per_cu > 0) g = std::min<int64_t>(g, static_cast<int64_t>(ctx->num_cus) * wgs_per_cu);
+  return std::max<int64_t>(1, std::min<int64_t>(g, cap));
 }
 
-template <bool TO_HOST, bool VEC, bool NT>
-hipError_t launch_swap_t(int64_t grid, hipStream_t st, const SegDesc* s, const EntDesc* e,
-                         const int64_t* k, uint32_t ns, uint32_t items, uint32_t cpt, char* hb,
-                         int64_t hs, int64_t hro) {
-  hipLaunchKernelGGL((swap_tiles_kernel<TO_HOST, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(kWG), 0, st, s, e, k, ns, items, cpt, hb, hs, hro);
+struct SwapArgs {
+  const SegDesc* segs;
+  const EntDesc* ents;
+  const int64_t* kpp;
+  uint32_t num_segs, num_items, cpt;
+  char* host_base;
+  int64_t host_stride, host_rank_offset;
+};
+
+template <int WG, int U, bool TO_HOST, bool VEC, bool NT>
+hipError_t launch_swap_t(int64_t grid, hipStream_t st, const SwapArgs& a) {
+  hipLaunchKernelGGL((swap_tiles_kernel<WG, U, TO_HOST, VEC, NT>),
+                     dim3(static_cast<uint32_t>(grid)), dim3(WG), 0, st, a.segs, a.ents, a.kpp,
+                     a.num_segs, a.num_items, a.cpt, a.host_base, a.host_stride,
+                     a.host_rank_offset);
   return hipGetLastError();
 }
 
-hipError_t launch_swap(bool to_host, bool vec, bool nt, int64_t grid, hipStream_t st,
-                       const SegDesc* s, const EntDesc* e, const int64_t* k, uint32_t ns,
-                       uint32_t items, uint32_t cpt, char* hb, int64_t hs, int64_t hro) {
-#define AEGKV_L(A, B, C) \
-  return launch_swap_t<A, B, C>(grid, st, s, e, k, ns, items, cpt, hb, hs, hro)
-  if (to_host) {
-    if (vec) {
-      if (nt) AEGKV_L(true, true, true);
-      AEGKV_L(true, true, false);
-    }
-    AEGKV_L(true, false, false);
-  }
-  if (vec) {
-    if (nt) AEGKV_L(false, true, true);
-    AEGKV_L(false, true, false);
-  }
-  AEGKV_L(false, false, false);
-#undef AEGKV_L
+template <int WG, int U>
+hipError_t launch_swap_shape(bool to_host, bool nt, int64_t grid, hipStream_t st,
+                             const SwapArgs& a) {
+  if (to_host)
+    return nt ? launch_swap_t<WG, U, true, true, true>(grid, st, a)
+              : launch_swap_t<WG, U, true, true, false>(grid, st, a);
+  return nt ? launch_swap_t<WG, U, false, true, true>(grid, st, a)
+            : launch_swap_t<WG, U, false, true, false>(grid, st, a);
 }
 
-hipError_t launch_copy(bool vec, bool nt, int64_t grid, hipStream_t st, const SegDesc* s,
-                       const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
-  const dim3 g(static_cast<uint32_t>(grid)), b(kWG);
-  if (vec) {
-    if (nt)
-      hipLaunchKernelGGL((copy_blocks_kernel<true, true>), g, b, 0, st, s, p, ns, items, cpt);
-    else
-      hipLaunchKernelGGL((copy_blocks_kernel<true, false>), g, b, 0, st, s, p, ns, items, cpt);
-  } else {
-    hipLaunchKernelGGL((copy_blocks_kernel<false, false>), g, b, 0, st, s, p, ns, items, cpt);
-  }
+hipError_t launch_swap(ShapeSel sh, bool to_host, bool vec, bool nt, int64_t grid,
+                       hipStream_t st, const SwapArgs& a) {
+  if (!vec)
+    return to_host ? launch_swap_t<256, 1, true, false, false>(grid, st, a)
+                   : launch_swap_t<256, 1, false, false, false>(grid, st, a);
+#define AEGKV_SW(W, UU) \
+  if (sh.wg == W && sh.u == UU) return launch_swap_shape<W, UU>(to_host, nt, grid, st, a);
+  AEGKV_SW(256, 1) AEGKV_SW(256, 2) AEGKV_SW(256, 4)
+  AEGKV_SW(1024, 1) AEGKV_SW(1024, 2) AEGKV_SW(1024, 3) AEGKV_SW(1024, 4)
+  AEGKV_SW(1024, 5) AEGKV_SW(1024, 6) AEGKV_SW(1024, 8) AEGKV_SW(1024, 10)
+#undef AEGKV_SW
+  return hipErrorInvalidValue;
+}
+
+template <int WG, int U, bool VEC, bool NT>
+hipError_t launch_copy_t(int64_t grid, hipStream_t st, const SegDesc* s, const PairDesc* p,
+                         uint32_t ns, uint32_t items, uint32_t cpt) {
+  hipLaunchKernelGGL((copy_blocks_kernel<WG, U, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(WG), 0, st, s, p, ns, items, cpt);
   return hipGetLastError();
+}
+
+hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, hipStream_t st,
+                       const SegDesc* s, const PairDesc* p, uint32_t ns, uint32_t items,
+                       uint32_t cpt) {
+  if (!vec) return launch_copy_t<256, 1, false, false>(grid, st, s, p, ns, items, cpt);
+#define AEGKV_CP(W, UU)                                                          \
+  if (sh.wg == W && sh.u == UU)                                                  \
+    return nt ? launch_copy_t<W, UU, true, true>(grid, st, s, p, ns, items, cpt) \
+              : launch_copy_t<W, UU, true, false>(grid, st, s, p, ns, items, cpt);
+  AEGKV_CP(256, 1) AEGKV_CP(256, 2) AEGKV_CP(256, 4)
+  AEGKV_CP(1024, 1) AEGKV_CP(1024, 2) AEGKV_CP(1024, 3) AEGKV_CP(1024, 4)
+  AEGKV_CP(1024, 5) AEGKV_CP(1024, 6) AEGKV_CP(1024, 8) AEGKV_CP(1024, 10)
+#undef AEGKV_CP
+  return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------ swap core --
@@ -616,7 +681,10 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
     he[j] = d;
   }
   char* dv = ctx->ring.dev + off;
-  const int64_t cpt = (max_page + kChunk - 1) / kChunk;
+  const Tunables t = tunables();
+  const ShapeSel sh = !vec ? ShapeSel{256, 1}
+                           : (t.swap_shape_auto ? auto_shape(max_page) : ShapeSel{256, 4});
+  const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
   const int64_t items = n * S * cpt;
   if (items >= (int64_t(1) << 32)) {
     ctx->ring.head = off;  // nothing was enqueued; hand the region back
@@ -625,13 +693,15 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   }
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
-  const Tunables t = tunables();
-  e = launch_swap(!is_swap_in, vec, t.nt_stores != 0, grid_for(ctx, items), stream,
-                  reinterpret_cast<const SegDesc*>(dv),
-                  reinterpret_cast<const EntDesc*>(dv + ent_off),
-                  reinterpret_cast<const int64_t*>(dv + kpp_off), static_cast<uint32_t>(S),
-                  static_cast<uint32_t>(items), static_cast<uint32_t>(cpt), host_side,
-                  host_stride, host_rank_off);
+  SwapArgs a{reinterpret_cast<const SegDesc*>(dv), reinterpret_cast<const EntDesc*>(dv + ent_off),
+             reinterpret_cast<const int64_t*>(dv + kpp_off), static_cast<uint32_t>(S),
+             static_cast<uint32_t>(items), static_cast<uint32_t>(cpt), host_side, host_stride,
+             host_rank_off};
+  // Non-temporal stores only where the destination is HBM: plain stores to
+  // the host pool measured faster (no L2 residency to avoid there).
+  const bool nt = t.nt_stores != 0 && !(!is_swap_in && !staged);
+  e = launch_swap(sh, !is_swap_in, vec, nt, launch_grid(ctx, t.wgs_per_cu, items, sh.wg),
+                  stream, a);
   if (e != hipSuccess) return hip_fail(e, "swap_tiles_kernel launch");
   return ring_commit(ctx->ring, off, total, stream);
 }
@@ -754,6 +824,9 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_AUTO_D2H: slot = &g_tune.auto_d2h; break;
     case AEGKV_TUNE_AUTO_H2D: slot = &g_tune.auto_h2d; break;
     case AEGKV_TUNE_NT_STORES: slot = &g_tune.nt_stores; break;
+    case AEGKV_TUNE_COPY_WGS_PER_CU: slot = &g_tune.copy_wgs_per_cu; break;
+    case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
+    case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -765,6 +838,12 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "workgroups per CU must be in [1, 64]");
     if (key == AEGKV_TUNE_STAGING_BYTES && value < (int64_t(1) << 20))
       return fail(AEGKV_EINVAL, "staging must be at least 1 MiB");
+    if (key == AEGKV_TUNE_COPY_WGS_PER_CU && value > 64)
+      return fail(AEGKV_EINVAL, "copy workgroups per CU must be in [0, 64]");
+    if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && !valid_copy_unroll(value))
+      return fail(AEGKV_EINVAL, "copy unroll must be 0 (auto) or one of 1,2,3,4,5,6,8,10");
+    if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
+      return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
     *slot = value;
   }
   return prev;
@@ -856,7 +935,11 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
     role[static_cast<size_t>(s)] = 1;
   }
   if (num_pairs == 0) return 0;
-  const int64_t cpt = (max_page + kChunk - 1) / kChunk;
+  const Tunables t = tunables();
+  ShapeSel sh = auto_shape(max_page);
+  if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};
+  if (!vec) sh = ShapeSel{256, 1};
+  const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
   const int64_t items = num_pairs * num_segments * cpt;
   if (items >= (int64_t(1) << 32))
     return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
@@ -880,8 +963,8 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
   char* dv = ctx->ring.dev + off;
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
-  const Tunables t = tunables();
-  e = launch_copy(vec, t.nt_stores != 0, grid_for(ctx, items), stream,
+  e = launch_copy(sh, vec, t.nt_stores != 0,
+                  launch_grid(ctx, t.copy_wgs_per_cu, items, sh.wg), stream,
                   reinterpret_cast<const SegDesc*>(dv),
                   reinterpret_cast<const PairDesc*>(dv + pair_off),
                   static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),

@@ -55,7 +55,13 @@ extern "C" {
 #define AEGKV_TUNE_STAGING_BYTES 2   /* max device staging per chunk      */
 #define AEGKV_TUNE_AUTO_D2H 3        /* mode AUTO picks for swap-out      */
 #define AEGKV_TUNE_AUTO_H2D 4        /* mode AUTO picks for swap-in       */
-#define AEGKV_TUNE_NT_STORES 5       /* 1: non-temporal stores in copies  */
+#define AEGKV_TUNE_NT_STORES 5       /* 1: non-temporal stores to HBM     */
+#define AEGKV_TUNE_COPY_WGS_PER_CU 6 /* copy_blocks grid: 0 = one workgroup
+                                        per work item, else per-CU count   */
+#define AEGKV_TUNE_COPY_UNROLL 7     /* copy_blocks loads per lane: 0 = from
+                                        the page size, else 1-6, 8 or 10   */
+#define AEGKV_TUNE_SWAP_SHAPE_AUTO 8 /* 1: swap kernels pick their shape
+                                        from the page size like copy_blocks */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -180,6 +180,80 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
     assert np.array_equal(seg.cpu().numpy(), segs_np[4])
 
 
+@pytest.fixture
+def restore_tuning():
+    keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
+            _lib.TUNE_WGS_PER_CU, _lib.TUNE_NT_STORES)
+    saved = {k: _lib.tune(k) for k in keys}
+    yield
+    for k, v in saved.items():
+        _lib.tune(k, v)
+
+
+def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
+    """Every instantiated copy shape and both grid policies, on tiles that
+    divide evenly, leave tails, or are smaller than one row."""
+    rng = np.random.default_rng(21)
+    n = 24
+    page = np.array([160 * 1024, 48 * 1024 + 16, 4096, 32 * 1024, 112], np.int64)
+    for unroll in (0, 1, 2, 3, 4, 5, 6, 8, 10):
+        for wpc in (0, 3):
+            _lib.tune(_lib.TUNE_COPY_UNROLL, unroll)
+            _lib.tune(_lib.TUNE_COPY_WGS_PER_CU, wpc)
+            segs_np = [rng.integers(0, 256, (n, int(p)), dtype=np.uint8) for p in page[:4]]
+            perm = rng.permutation(n)
+            src, dst = perm[:9], perm[9:18]
+            segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+            ops.copy_blocks(segs, src, dst)
+            oracle.copy_blocks([x.reshape(-1) for x in segs_np], page[:4], n, src, dst)
+            torch.cuda.synchronize()
+            for s in range(4):
+                assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (unroll, wpc, s)
+
+
+@pytest.mark.parametrize("shape_auto", [0, 1])
+@pytest.mark.parametrize("wpc", [1, 8, 64])
+def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, wpc):
+    _lib.tune(_lib.TUNE_SWAP_SHAPE_AUTO, shape_auto)
+    _lib.tune(_lib.TUNE_WGS_PER_CU, wpc)
+    rng = np.random.default_rng(31 + wpc)
+    page = np.array([160 * 1024, 32 * 1024, 4096, 48 * 1024 + 16 * 4], np.int64)
+    cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)
+    owners = np.array([1, 3, 2, 1], np.uint64)
+    kpp = np.array([1, 4], np.int64)
+    composite = int(page.sum())
+    n_gpu, n_host, n = 20, 16, 10
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    grp = rng.integers(0, 2, n).astype(np.int32)
+    first = np.array([0 if g == 0 else rng.integers(0, 4) for g in grp], np.int64)
+    valid = np.array([1 if g == 0 else rng.integers(0, 4 - f + 1) for g, f in zip(grp, first)],
+                     np.int64)
+    src, dst = rng.permutation(n_gpu)[:n], rng.permutation(n_host)[:n]
+    for mode in MODES:
+        segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+        pool = ops.PinnedHostPool(n_host * composite)
+        pool.tensor.zero_()
+        ops.swap_segments(segs, page, cpu_off, owners, n_gpu, kpp, pool.tensor, composite, 0,
+                          src, dst, grp, first, valid, False, mode=mode)
+        want = np.zeros((n_host, composite), np.uint8)
+        oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                           want.reshape(-1), composite, 0, composite, src, dst, grp, first,
+                           valid, False)
+        torch.cuda.synchronize()
+        assert np.array_equal(pool.tensor.numpy().reshape(want.shape), want), mode
+        back = rng.permutation(n_gpu)[:n]
+        ops.swap_segments(segs, page, cpu_off, owners, n_gpu, kpp, pool.tensor, composite, 0,
+                          dst, back, grp, first, valid, True, mode=mode)
+        want_segs = [x.copy() for x in segs_np]
+        oracle.swap_blocks([x.reshape(-1) for x in want_segs], page, cpu_off, owners, n_gpu,
+                           kpp, want.reshape(-1), composite, 0, composite, dst, back, grp, first,
+                           valid, True)
+        torch.cuda.synchronize()
+        for s in range(len(page)):
+            assert np.array_equal(segs[s].cpu().numpy(), want_segs[s]), (mode, s)
+        pool.free()
+
+
 # --------------------------------------------------------- error behaviour --
 
 def test_rejections_enqueue_nothing(gpu):
