@@ -1,0 +1,238 @@
+"""Swap planning: destination allocation and the per-move copy lists.
+
+Synchronous mirror of the planning half of the reference's BlockManager:
+the GPU free lists (aegaeon/block_manager.py:718-793, 956-974), the CPU slab
+allocator (:653-659, 976-1029), the move planner of move_requests
+(:1355-1478) and the reclamation of a finished move's source blocks
+(:663-690). Ray RPC, asyncio waits and CUDA events are not part of it: a
+caller runs the returned SwapPlan through KVSwapper.swap_blocks (or the C
+ABI) and calls BlockPools.reclaim(plan) once the move's event has completed.
+"""
+
+from __future__ import annotations
+
+import math
+from collections import defaultdict, deque
+from dataclasses import dataclass, field
+from typing import Deque, Dict, List, Optional, Sequence, Tuple
+
+from .cache_groups import (
+    BLOCK_LOCATION_CPU,
+    VLLM_NULL_BLOCK_ID,
+    BlockTable,
+    CacheGroupConfig,
+    is_gpu,
+)
+
+
+def slab_range(slab: int, slab_size_bytes: int, block_size_bytes: int) -> Tuple[int, int]:
+    """Host block ids wholly inside slab `slab` (block_manager.py:656-659):
+    [ceil(slab * S / B), floor((slab + 1) * S / B))."""
+    start = -(-(slab * slab_size_bytes) // block_size_bytes)
+    end = ((slab + 1) * slab_size_bytes) // block_size_bytes
+    return start, end
+
+
+class BlockPools:
+    """Free block ids per location: GPU engines and the CPU slab pool."""
+
+    def __init__(self, cpu_num_slabs: int, cpu_slab_size_bytes: int, dtype_size: int = 2):
+        if cpu_num_slabs < 0 or cpu_slab_size_bytes <= 0:
+            raise ValueError("slab geometry must be positive")
+        self.dtype_size = dtype_size
+        self.cpu_num_slabs = cpu_num_slabs
+        self.cpu_slab_size_bytes = cpu_slab_size_bytes
+        self.cpu_free_blocks: Dict[Tuple[int, ...], Deque[int]] = defaultdict(deque)
+        self.cpu_free_slabs: List[int] = list(range(cpu_num_slabs))
+        self.cpu_slab_usage: List[int] = [0] * cpu_num_slabs
+        self.cpu_block_shape: List[Optional[Tuple[int, ...]]] = [None] * cpu_num_slabs
+        self.gpu_free_blocks: Dict[int, List[int]] = {}
+        self.gpu_block_shape: Dict[int, Tuple[int, ...]] = {}
+        self.gpu_cache_groups: Dict[int, Tuple[CacheGroupConfig, ...]] = {}
+
+    def block_size_bytes(self, block_shape: Tuple[int, ...]) -> int:
+        return math.prod(block_shape) * self.dtype_size
+
+    def register_gpu_space(self, engine_id: int, num_max_blocks: int,
+                           block_shape: Tuple[int, ...],
+                           cache_groups: Sequence[CacheGroupConfig]) -> None:
+        """Expose device ids 1..num_max_blocks-1 (block 0 is vLLM's null
+        block), as block_manager.py:775-792 does."""
+        if num_max_blocks <= 1:
+            raise ValueError(
+                "GPU cache must contain at least one usable block in addition to the "
+                "reserved null block"
+            )
+        if not cache_groups:
+            raise ValueError("GPU cache must expose at least one cache group")
+        self.gpu_block_shape[engine_id] = tuple(block_shape)
+        self.gpu_cache_groups[engine_id] = tuple(cache_groups)
+        self.gpu_free_blocks[engine_id] = list(range(VLLM_NULL_BLOCK_ID + 1, num_max_blocks))
+
+    def _cpu_blocks_available(self, block_bytes: int, needed: int) -> bool:
+        if needed <= 0:
+            return True
+        for slab in self.cpu_free_slabs:
+            lo, hi = slab_range(slab, self.cpu_slab_size_bytes, block_bytes)
+            needed -= hi - lo
+            if needed <= 0:
+                return True
+        return False
+
+    def allocate(self, num_blocks: int, location: int,
+                 block_shape: Tuple[int, ...]) -> List[int]:
+        """Reserve `num_blocks` ids at `location` (block_manager.py:942-1031).
+
+        GPU: the FIFO prefix of the engine's free list. CPU: the shape's free
+        deque, refilled from free slabs taken from the end of the slab list;
+        each id lies wholly inside one slab. Raises ResourceWarning when the
+        location cannot supply the ids (nothing is reserved then).
+        """
+        if num_blocks < 0:
+            raise ValueError("num_blocks must be >= 0")
+        block_shape = tuple(block_shape)
+        if is_gpu(location):
+            if location not in self.gpu_free_blocks:
+                raise KeyError(f"unknown gpu location {location}")
+            free = self.gpu_free_blocks[location]
+            if len(free) < num_blocks:
+                raise ResourceWarning(
+                    f"not enough free blocks on GPU, requested {num_blocks}, "
+                    f"available {len(free)}"
+                )
+            out = free[:num_blocks]
+            del free[:num_blocks]
+            return out
+        block_bytes = self.block_size_bytes(block_shape)
+        free = self.cpu_free_blocks[block_shape]
+        if not self._cpu_blocks_available(block_bytes, num_blocks - len(free)):
+            raise ResourceWarning(
+                f"not enough free blocks on CPU, requested {num_blocks}, available "
+                f"{len(free)} and {len(self.cpu_free_slabs)} slabs"
+            )
+        while len(free) < num_blocks:
+            slab = self.cpu_free_slabs.pop()
+            lo, hi = slab_range(slab, self.cpu_slab_size_bytes, block_bytes)
+            self.cpu_block_shape[slab] = block_shape
+            free.extend(range(lo, hi))
+        out = []
+        for _ in range(num_blocks):
+            b = free.popleft()
+            self.cpu_slab_usage[b * block_bytes // self.cpu_slab_size_bytes] += 1
+            out.append(b)
+        return out
+
+    def release(self, blocks: Sequence[int], location: int,
+                block_shape: Tuple[int, ...]) -> None:
+        """Return ids to their free list (block_manager.py:663-690)."""
+        if is_gpu(location):
+            self.gpu_free_blocks[location].extend(blocks)
+            return
+        block_shape = tuple(block_shape)
+        block_bytes = self.block_size_bytes(block_shape)
+        self.cpu_free_blocks[block_shape].extend(blocks)
+        for b in blocks:
+            self.cpu_slab_usage[b * block_bytes // self.cpu_slab_size_bytes] -= 1
+
+    def reclaim(self, plan: "SwapPlan") -> None:
+        """Free a completed move's source ids (all of them, including pages
+        that were not copied)."""
+        self.release(plan.release_source_block_ids, plan.source_location, plan.block_shape)
+
+
+@dataclass
+class SwapPlan:
+    """One swap_blocks call's lists plus the bookkeeping of the move."""
+
+    request_ids: List[int]
+    source_location: int
+    target_location: int
+    block_shape: Tuple[int, ...]
+    source_block_ids: List[int] = field(default_factory=list)
+    target_block_ids: List[int] = field(default_factory=list)
+    group_ids: List[int] = field(default_factory=list)
+    first_kernel_blocks: List[int] = field(default_factory=list)
+    valid_kernel_blocks: List[int] = field(default_factory=list)
+    release_source_block_ids: List[int] = field(default_factory=list)
+
+    @property
+    def is_swap_in(self) -> bool:
+        return is_gpu(self.target_location)
+
+    @property
+    def engine_id(self) -> int:
+        """The GPU side of the swap, whose worker runs it."""
+        return self.target_location if is_gpu(self.target_location) else self.source_location
+
+
+def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, BlockTable],
+              target_location: int, pools: BlockPools) -> Optional[SwapPlan]:
+    """Plan moving requests' blocks to `target_location`
+    (block_manager.py:1355-1478).
+
+    requests: (request_id, processed_computed_tokens) pairs; duplicates are
+    ignored, requests already at the target are skipped. All moved requests
+    must share one source location and block shape. Destinations for every
+    retained page are reserved in one allocation before any table changes;
+    pages with nothing to copy get a destination but stay out of the copy
+    lists; the tables are rewritten to the destination. Returns None when
+    nothing moves.
+    """
+    seen = set()
+    plans = []
+    src_loc: Optional[int] = None
+    shape: Optional[Tuple[int, ...]] = None
+    moved_ids: List[int] = []
+    release: List[int] = []
+    for rid, tokens in requests:
+        if rid in seen:
+            continue
+        seen.add(rid)
+        table = block_tables.get(rid)
+        if table is None:
+            raise KeyError(f"request {rid} not allocated")
+        if table.location == target_location:
+            continue
+        if is_gpu(table.location) and is_gpu(target_location):
+            raise NotImplementedError("Migration is not implemented")
+        if src_loc is not None and table.location != src_loc:
+            raise ValueError(f"request {rid} is on {table.location}; expected {src_loc}")
+        if shape is not None and tuple(table.block_shape) != shape:
+            raise ValueError(f"request {rid}'s shape is not {shape}")
+        src_loc = table.location
+        shape = tuple(table.block_shape)
+        if is_gpu(target_location):
+            groups = pools.gpu_cache_groups.get(target_location)
+            if tuple(table.cache_groups) != groups:
+                raise ValueError(
+                    f"request {rid} cache groups do not match target engine #{target_location}"
+                )
+        entries = table.transfer_entries(tokens)
+        plans.append((table, tokens, entries))
+        moved_ids.append(rid)
+        release += table.blocks
+    if not plans:
+        return None
+    targets = pools.allocate(sum(len(e) for _, _, e in plans), target_location, shape)
+    plan = SwapPlan(moved_ids, src_loc, target_location, shape,
+                    release_source_block_ids=release)
+    cursor = 0
+    new_tables = []
+    for table, tokens, entries in plans:
+        mine = targets[cursor:cursor + len(entries)]
+        cursor += len(entries)
+        for (g, _, pid, first, count), tid in zip(entries, mine):
+            if count > 0:
+                plan.source_block_ids.append(pid)
+                plan.target_block_ids.append(tid)
+                plan.group_ids.append(g)
+                plan.first_kernel_blocks.append(first)
+                plan.valid_kernel_blocks.append(count)
+        new_tables.append(table.moved_group_blocks(tokens, mine))
+    for (table, _, _), groups in zip(plans, new_tables):
+        table.group_blocks = groups
+        table.location = target_location
+    return plan
+
+
+__all__ = ["BLOCK_LOCATION_CPU", "BlockPools", "SwapPlan", "plan_move", "slab_range"]

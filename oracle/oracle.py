@@ -14,6 +14,10 @@ Parity status per function (the checks live in tests/test_oracle.py):
   kernel_block_extent, byte_extent and the cache_transfer helpers: pinned by
     brute force over token positions, the reference's docstring known
     answers and its benchmark's extent plans.
+  slab_range, plan_lists (tests/test_planner.py): pinned by invariants the
+    reference's allocator and planner guarantee - a host page never
+    straddles a slab, targets are distinct, every retained page appears
+    once, pages with nothing to copy get a destination but no copy entry.
 No function is "parity unpinned".
 """
 
@@ -238,3 +242,38 @@ def swap_blocks_torch(gpu_pages, host_view, segment_cpu_offsets, segment_owners,
             else:
                 host_view[dst].narrow(0, hoff, ln).copy_(pages[src].narrow(0, off, ln))
     return copied, ops
+
+
+# ----------------------------------------------------------- move planning --
+
+def slab_range(slab: int, slab_size_bytes: int, block_size_bytes: int) -> tuple[int, int]:
+    """aegaeon/block_manager.py:656-659, with its float division."""
+    import math
+
+    return (math.ceil(slab * slab_size_bytes / block_size_bytes),
+            math.floor((slab + 1) * slab_size_bytes / block_size_bytes))
+
+
+def plan_lists(per_table_entries, targets):
+    """aegaeon/block_manager.py:1439-1470: split the reserved `targets`
+    across the tables in order; copy lists keep only entries with count > 0;
+    each table's destination columns get their target ids (released columns
+    stay -1). per_table_entries[i] = (entries, columns_per_group) with
+    entries as BlockTable.transfer_entries rows."""
+    src, dst, grp, first, valid, tables = [], [], [], [], [], []
+    cursor = 0
+    for entries, cols in per_table_entries:
+        new_ids = targets[cursor:cursor + len(entries)]
+        cursor += len(entries)
+        for entry, t in zip(entries, new_ids):
+            if entry[4] > 0:
+                src.append(entry[2])
+                dst.append(t)
+                grp.append(entry[0])
+                first.append(entry[3])
+                valid.append(entry[4])
+        moved = [[-1] * n for n in cols]
+        for entry, t in zip(entries, new_ids):
+            moved[entry[0]][entry[1]] = t
+        tables.append(moved)
+    return src, dst, grp, first, valid, tables

@@ -368,6 +368,78 @@ def test_swapper_block_table_round_trip(gpu, oracle):
     pool.free()
 
 
+def test_planner_swap_out_and_back_in(gpu):
+    """plan_move -> KVSwapper out to the host pool, reclaim, plan_move ->
+    KVSwapper back in: every live extent of every retained page arrives at
+    its new device id unchanged."""
+    import random
+
+    from aegaeon_amd.cache_groups import CacheGroupConfig, CacheGroupRuntimeConfig, BlockTable
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.planner import BLOCK_LOCATION_CPU, BlockPools, plan_move
+    from aegaeon_amd.swapper import KVSwapper
+
+    rng = random.Random(4)
+    n_blocks = 256
+    groups = (CacheGroupConfig("attention", 32, 16), CacheGroupConfig("attention", 32, 16, 24))
+    descr = [CacheGroupRuntimeConfig("attention", 32, 16),
+             CacheGroupRuntimeConfig("attention", 32, 16, 24)]
+    specs = [KVCacheTensorSpec(n_blocks * 2048, ("full.0",)),
+             KVCacheTensorSpec(n_blocks * 2048, ("win.0",)),
+             KVCacheTensorSpec(n_blocks * 4096, ("full.1", "win.1"))]
+    cache = allocate_composite_cache(specs, n_blocks, gpu)
+    for t in cache.backing:
+        t.random_(-128, 127)
+    shape = (cache.page_size_bytes // 2,)
+    slab = 4 * cache.page_size_bytes + 100
+    pools = BlockPools(cpu_num_slabs=40, cpu_slab_size_bytes=slab)
+    pools.register_gpu_space(0, n_blocks, shape, groups)
+    host = ops.PinnedHostPool(40 * slab)
+    sw = KVSwapper(cache, [{"full.0", "full.1"}, {"win.0", "win.1"}], descr, host.tensor)
+    tables, reqs = {}, []
+    for rid in range(5):
+        tokens = rng.randint(1, 150)
+        cols = [groups[0].table_blocks_for_tokens(tokens), groups[1].table_blocks_for_tokens(tokens)]
+        ids = pools.allocate(sum(cols), 0, shape)
+        tables[rid] = BlockTable(0, shape, groups, [ids[:cols[0]], ids[cols[0]:]])
+        tables[rid].release_skipped_blocks(tokens)
+        reqs.append((rid, tokens))
+    before = [t.clone() for t in cache.backing]
+    orig = {rid: [list(c) for c in tables[rid].group_blocks] for rid, _ in reqs}
+    out = plan_move(reqs, tables, BLOCK_LOCATION_CPU, pools)
+    ev = sw.swap_blocks(out.request_ids, out.source_block_ids, out.target_block_ids,
+                        out.group_ids, out.first_kernel_blocks, out.valid_kernel_blocks,
+                        [None] * len(out.request_ids), False)
+    ev.synchronize()
+    pools.reclaim(out)
+    back = plan_move(reqs, tables, 0, pools)
+    ev2 = sw.swap_blocks(back.request_ids, back.source_block_ids, back.target_block_ids,
+                         back.group_ids, back.first_kernel_blocks, back.valid_kernel_blocks,
+                         [ev] * len(back.request_ids), True)
+    ev2.synchronize()
+    pools.reclaim(back)
+    owners = [(0, 0), (1, 1), (2, 0), (2, 1)]  # (backing tensor, group)
+    pages = [2048, 2048, 4096]
+    checked = 0
+    for rid, tokens in reqs:
+        for g in range(2):
+            for col, (old, new) in enumerate(zip(orig[rid][g], tables[rid].group_blocks[g])):
+                if old < 0:
+                    continue
+                first, count = groups[g].kernel_block_extent(tokens, col)
+                for seg, og in owners:
+                    if og != g:
+                        continue
+                    unit = pages[seg] // 2
+                    lo, hi = unit * first, unit * (first + count)
+                    a = before[seg].view(n_blocks, pages[seg])[old, lo:hi]
+                    b = cache.backing[seg].view(n_blocks, pages[seg])[new, lo:hi]
+                    assert torch.equal(a, b), (rid, g, col, seg)
+                    checked += 1
+    assert checked > 20
+    host.free()
+
+
 # ---------------------------------------------------- full benchmark shapes --
 
 def _kv_segments(n_layers, n_blocks, heads, dim, dtype, dev, seed):

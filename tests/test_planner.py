@@ -1,0 +1,142 @@
+"""Swap planning: allocation and copy lists (CPU only)."""
+
+import copy
+import random
+
+import pytest
+
+from aegaeon_amd.cache_groups import LOGICAL_NULL_BLOCK_ID, BlockTable, CacheGroupConfig
+from aegaeon_amd.planner import BLOCK_LOCATION_CPU, BlockPools, plan_move, slab_range
+
+GROUPS = (CacheGroupConfig("attention", 32, 16),
+          CacheGroupConfig("attention", 32, 16, sliding_window=40),
+          CacheGroupConfig("mamba_none", 1, 1))
+SHAPE = (1000,)  # 2000-byte host blocks
+
+
+def test_slab_range_matches_reference_formula(oracle):
+    for slab_bytes in (4096, 1 << 20, 3 * 7 * 1000):
+        for block in (2000, 2048, 4096, 2_359_296, 3_145_728):
+            for slab in range(0, 40):
+                assert slab_range(slab, slab_bytes, block) == oracle.slab_range(slab, slab_bytes, block)
+
+
+def test_cpu_blocks_never_straddle_slabs():
+    pools = BlockPools(cpu_num_slabs=6, cpu_slab_size_bytes=7000)
+    got = pools.allocate(12, BLOCK_LOCATION_CPU, SHAPE)
+    assert len(set(got)) == 12
+    for b in got:
+        # bytes [b*2000, (b+1)*2000) inside one 7000-byte slab
+        assert b * 2000 // 7000 == ((b + 1) * 2000 - 1) // 7000
+    # slabs are taken from the end of the slab list, ids ascend inside a slab
+    assert got[:3] == list(range(*slab_range(5, 7000, 2000)))
+    assert sum(pools.cpu_slab_usage) == 12
+    with pytest.raises(ResourceWarning):
+        pools.allocate(100, BLOCK_LOCATION_CPU, SHAPE)
+    pools.release(got[:5], BLOCK_LOCATION_CPU, SHAPE)
+    assert sum(pools.cpu_slab_usage) == 7
+
+
+def test_gpu_free_list_fifo_and_null_block():
+    pools = BlockPools(1, 1 << 20)
+    pools.register_gpu_space(0, 10, SHAPE, GROUPS)
+    assert pools.allocate(3, 0, SHAPE) == [1, 2, 3]
+    assert pools.allocate(2, 0, SHAPE) == [4, 5]
+    with pytest.raises(ResourceWarning):
+        pools.allocate(5, 0, SHAPE)
+    pools.release([2, 4], 0, SHAPE)
+    assert pools.allocate(6, 0, SHAPE) == [6, 7, 8, 9, 2, 4]
+    with pytest.raises(ValueError):
+        pools.register_gpu_space(1, 1, SHAPE, GROUPS)
+
+
+def _tables(rng, n_req, pools):
+    tables = {}
+    reqs = []
+    for rid in range(n_req):
+        tokens = rng.randint(1, 200)
+        cols = [GROUPS[0].table_blocks_for_tokens(tokens), GROUPS[1].table_blocks_for_tokens(tokens), 1]
+        ids = pools.allocate(sum(cols), 0, SHAPE)
+        it = iter(ids)
+        groups = [[next(it) for _ in range(c)] for c in cols]
+        t = BlockTable(0, SHAPE, GROUPS, groups)
+        t.release_skipped_blocks(tokens)
+        tables[rid] = t
+        reqs.append((rid, tokens))
+    return tables, reqs
+
+
+@pytest.mark.parametrize("seed", range(5))
+def test_plan_move_matches_reference_list_building(oracle, seed):
+    rng = random.Random(seed)
+    pools = BlockPools(cpu_num_slabs=64, cpu_slab_size_bytes=1 << 16)
+    pools.register_gpu_space(0, 4096, SHAPE, GROUPS)
+    tables, reqs = _tables(rng, 6, pools)
+    before = copy.deepcopy(tables)
+    reqs = reqs + [reqs[0]]  # duplicate request id is ignored
+    plan = plan_move(reqs, tables, BLOCK_LOCATION_CPU, pools)
+    per_table = []
+    for rid, tokens in reqs[:-1]:
+        t = before[rid]
+        per_table.append((t.transfer_entries(tokens), [len(c) for c in t.group_blocks]))
+    n_targets = sum(len(e) for e, _ in per_table)
+    # the reserved targets are exactly what a fresh pool hands out in order
+    fresh = BlockPools(cpu_num_slabs=64, cpu_slab_size_bytes=1 << 16)
+    targets = fresh.allocate(n_targets, BLOCK_LOCATION_CPU, SHAPE)
+    src, dst, grp, first, valid, new_tables = oracle.plan_lists(per_table, targets)
+    assert plan.source_block_ids == src and plan.target_block_ids == dst
+    assert plan.group_ids == grp and plan.first_kernel_blocks == first
+    assert plan.valid_kernel_blocks == valid
+    for (rid, _), want in zip(reqs[:-1], new_tables):
+        assert tables[rid].group_blocks == want
+        assert tables[rid].location == BLOCK_LOCATION_CPU
+    assert sorted(plan.release_source_block_ids) == sorted(
+        b for rid, _ in reqs[:-1] for b in before[rid].blocks)
+    assert not plan.is_swap_in and plan.engine_id == 0
+    # every source page copied once, every target distinct
+    assert len(set(plan.target_block_ids)) == len(plan.target_block_ids)
+    # moving back plans a swap-in with the same extents
+    back = plan_move(reqs, tables, 0, pools)
+    assert back.is_swap_in and back.valid_kernel_blocks == plan.valid_kernel_blocks
+    assert back.source_block_ids == plan.target_block_ids
+    pools.reclaim(plan)
+
+
+def test_plan_move_rejections():
+    pools = BlockPools(cpu_num_slabs=8, cpu_slab_size_bytes=1 << 16)
+    pools.register_gpu_space(0, 64, SHAPE, GROUPS)
+    pools.register_gpu_space(1, 64, SHAPE, GROUPS[:1])
+    t0 = BlockTable(0, SHAPE, GROUPS, [[1], [2], [3]])
+    t1 = BlockTable(BLOCK_LOCATION_CPU, SHAPE, GROUPS, [[4], [5], [6]])
+    tables = {0: t0, 1: t1}
+    with pytest.raises(NotImplementedError):
+        plan_move([(0, 10)], tables, 1, pools)
+    tables[2] = BlockTable(1, SHAPE, GROUPS[:1], [[9]])
+    with pytest.raises(ValueError):
+        plan_move([(0, 10), (2, 10)], tables, BLOCK_LOCATION_CPU, pools)  # mixed sources
+    tables[3] = BlockTable(0, (999,), GROUPS, [[10], [11], [12]])
+    with pytest.raises(ValueError):
+        plan_move([(0, 10), (3, 10)], tables, BLOCK_LOCATION_CPU, pools)  # mixed shapes
+    with pytest.raises(ValueError):
+        plan_move([(1, 10)], tables, 1, pools)            # cache groups differ
+    with pytest.raises(KeyError):
+        plan_move([(7, 10)], tables, 0, pools)
+    assert plan_move([(0, 10)], tables, 0, pools) is None  # already there
+    small = BlockPools(cpu_num_slabs=1, cpu_slab_size_bytes=4000)
+    small.register_gpu_space(0, 64, SHAPE, GROUPS)
+    with pytest.raises(ResourceWarning):
+        plan_move([(0, 10)], {0: BlockTable(0, SHAPE, GROUPS, [[1, 2], [3], [4]])},
+                  BLOCK_LOCATION_CPU, small)
+
+
+def test_zero_count_pages_get_destinations_only():
+    """W = 1: the current page keeps a destination and no bytes move."""
+    groups = (CacheGroupConfig("attention", 16, 16, sliding_window=1),)
+    pools = BlockPools(cpu_num_slabs=4, cpu_slab_size_bytes=1 << 16)
+    pools.register_gpu_space(0, 64, SHAPE, groups)
+    tables = {0: BlockTable(0, SHAPE, groups, [[7, 8]])}
+    plan = plan_move([(0, 20)], tables, BLOCK_LOCATION_CPU, pools)
+    assert plan.source_block_ids == []
+    assert tables[0].group_blocks[0][0] == LOGICAL_NULL_BLOCK_ID
+    assert tables[0].group_blocks[0][1] >= 0
+    assert sorted(plan.release_source_block_ids) == [7, 8]
