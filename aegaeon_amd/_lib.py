@@ -31,7 +31,7 @@ MODE_AUTO = 0
 MODE_DIRECT = 1
 MODE_STAGED = 2
 
-TUNE_WGS_PER_CU = 1
+TUNE_SWAP_OUT_WORKGROUPS = 1
 TUNE_STAGING_BYTES = 2
 TUNE_AUTO_D2H = 3
 TUNE_AUTO_H2D = 4
@@ -39,6 +39,7 @@ TUNE_NT_STORES = 5
 TUNE_COPY_WGS_PER_CU = 6
 TUNE_COPY_UNROLL = 7
 TUNE_SWAP_SHAPE_AUTO = 8
+TUNE_SWAP_IN_WORKGROUPS = 9
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (

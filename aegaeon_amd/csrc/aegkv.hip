@@ -63,7 +63,11 @@ int hip_fail(hipError_t e, const char* what) {
 // --------------------------------------------------------------- tunables --
 
 struct Tunables {
-  int64_t wgs_per_cu = 8;        // swap kernels: persistent workgroups per CU
+  // Swap kernels: persistent workgroups in total, per direction. The swaps
+  // are link-bound; a few dozen workgroups saturate PCIe (more measured
+  // slower) and leave the other CUs to concurrent copies.
+  int64_t swap_out_workgroups = 32;
+  int64_t swap_in_workgroups = 64;
   int64_t staging_bytes = int64_t(512) << 20;
   int64_t auto_d2h = AEGKV_MODE_DIRECT;
   int64_t auto_h2d = AEGKV_MODE_DIRECT;
@@ -436,14 +440,14 @@ int check_host_range(const void* ptr, int64_t bytes, const char* what) {
 
 // ----------------------------------------------------------- launching --
 
-// Workgroups to launch: wgs_per_cu per CU striding over the items, or one
-// per item when wgs_per_cu is 0. An HSA dispatch counts work-items in 32
-// bits, so the grid is capped at (2^32 - 1) / lanes; the kernels' grid-stride
-// loops cover any remainder.
-int64_t launch_grid(const DeviceCtx* ctx, int64_t wgs_per_cu, int64_t items, int lanes) {
+// Workgroups to launch for `items` work items: at most `limit` when limit > 0
+// (the kernels' grid-stride loops cover the rest), else one per item. An HSA
+// dispatch counts work-items in 32 bits, so the grid is also capped at
+// (2^32 - 1) / lanes.
+int64_t launch_grid(int64_t limit, int64_t items, int lanes) {
   const int64_t cap = static_cast<int64_t>(UINT32_MAX) / lanes;
   int64_t g = items;
-  if (wgs_per_cu > 0) g = std::min<int64_t>(g, static_cast<int64_t>(ctx->num_cus) * wgs_per_cu);
+  if (limit > 0) g = std::min<int64_t>(g, limit);
   return std::max<int64_t>(1, std::min<int64_t>(g, cap));
 }
 
@@ -700,8 +704,8 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   // Non-temporal stores only where the destination is HBM: plain stores to
   // the host pool measured faster (no L2 residency to avoid there).
   const bool nt = t.nt_stores != 0 && !(!is_swap_in && !staged);
-  e = launch_swap(sh, !is_swap_in, vec, nt, launch_grid(ctx, t.wgs_per_cu, items, sh.wg),
-                  stream, a);
+  const int64_t wgs = is_swap_in ? t.swap_in_workgroups : t.swap_out_workgroups;
+  e = launch_swap(sh, !is_swap_in, vec, nt, launch_grid(wgs, items, sh.wg), stream, a);
   if (e != hipSuccess) return hip_fail(e, "swap_tiles_kernel launch");
   return ring_commit(ctx->ring, off, total, stream);
 }
@@ -819,7 +823,8 @@ int64_t aegkv_tune(int key, int64_t value) {
   std::lock_guard<std::mutex> lk(g_tune_mu);
   int64_t* slot = nullptr;
   switch (key) {
-    case AEGKV_TUNE_WGS_PER_CU: slot = &g_tune.wgs_per_cu; break;
+    case AEGKV_TUNE_SWAP_OUT_WORKGROUPS: slot = &g_tune.swap_out_workgroups; break;
+    case AEGKV_TUNE_SWAP_IN_WORKGROUPS: slot = &g_tune.swap_in_workgroups; break;
     case AEGKV_TUNE_STAGING_BYTES: slot = &g_tune.staging_bytes; break;
     case AEGKV_TUNE_AUTO_D2H: slot = &g_tune.auto_d2h; break;
     case AEGKV_TUNE_AUTO_H2D: slot = &g_tune.auto_h2d; break;
@@ -834,8 +839,9 @@ int64_t aegkv_tune(int key, int64_t value) {
     if ((key == AEGKV_TUNE_AUTO_D2H || key == AEGKV_TUNE_AUTO_H2D) &&
         value != AEGKV_MODE_DIRECT && value != AEGKV_MODE_STAGED)
       return fail(AEGKV_EINVAL, "AUTO must resolve to DIRECT or STAGED");
-    if (key == AEGKV_TUNE_WGS_PER_CU && (value < 1 || value > 64))
-      return fail(AEGKV_EINVAL, "workgroups per CU must be in [1, 64]");
+    if ((key == AEGKV_TUNE_SWAP_OUT_WORKGROUPS || key == AEGKV_TUNE_SWAP_IN_WORKGROUPS) &&
+        (value < 1 || value > 65536))
+      return fail(AEGKV_EINVAL, "swap workgroups must be in [1, 65536]");
     if (key == AEGKV_TUNE_STAGING_BYTES && value < (int64_t(1) << 20))
       return fail(AEGKV_EINVAL, "staging must be at least 1 MiB");
     if (key == AEGKV_TUNE_COPY_WGS_PER_CU && value > 64)
@@ -964,7 +970,7 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
   e = launch_copy(sh, vec, t.nt_stores != 0,
-                  launch_grid(ctx, t.copy_wgs_per_cu, items, sh.wg), stream,
+                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg), stream,
                   reinterpret_cast<const SegDesc*>(dv),
                   reinterpret_cast<const PairDesc*>(dv + pair_off),
                   static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),

@@ -51,6 +51,10 @@ def parse():
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--config", default="headline", choices=["headline", "varlen", "overlap"],
+                   help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
+                        "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
+                        "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams")
     return p.parse_args()
 
 
@@ -83,6 +87,34 @@ def measure_link(torch, ops, dev, nbytes=1 << 30, reps=3):
     del d
     pool.free()
     return out
+
+
+def measure_link_bidir(torch, ops, dev, nbytes=4 << 30):
+    """Both directions at once (two streams), aggregate GB/s."""
+    hp = [ops.PinnedHostPool(nbytes) for _ in range(2)]
+    dv = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(2)]
+    st = [torch.cuda.Stream() for _ in range(2)]
+    best = 0.0
+    for _ in range(3):
+        begin = torch.cuda.Event(enable_timing=True)
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        torch.cuda.synchronize()
+        begin.record()
+        for s_ in st:
+            s_.wait_event(begin)
+        with torch.cuda.stream(st[0]):
+            hp[0].tensor.copy_(dv[0], non_blocking=True)
+            ends[0].record()
+        with torch.cuda.stream(st[1]):
+            dv[1].copy_(hp[1].tensor, non_blocking=True)
+            ends[1].record()
+        torch.cuda.synchronize()
+        span = max(begin.elapsed_time(e) for e in ends) / 1e3
+        best = max(best, 2 * nbytes / span / 1e9)
+    del dv
+    for h in hp:
+        h.free()
+    return best
 
 
 def measure_stream_copy(torch, dev, nbytes=4 << 30, reps=3):
@@ -154,6 +186,214 @@ def cpu_baseline(runs: int):
     }
 
 
+def hip_streams(n):
+    """n new HIP streams from the HIP runtime torch loaded (hipStreamCreate)."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    out = []
+    for _ in range(n):
+        p = ctypes.c_void_p()
+        rc = hip.hipStreamCreate(ctypes.byref(p))
+        if rc != 0:
+            raise RuntimeError(f"hipStreamCreate failed ({rc})")
+        out.append(p.value)
+    return out
+
+
+def ev_pair(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def bench_varlen(args):
+    """Qwen2.5-7B KV shape (56 x [16384,16,4,128] bf16): 64 requests with
+    log-normal token lengths (median 1024, sigma 1.0, clipped to [16, 32768],
+    rounded up to 16-token blocks) whose blocks sit at seeded random device
+    ids; all of them swapped out in one batched call to host ids from the
+    slab allocator, then back in to fresh seeded device ids in one call."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+    from aegaeon_amd.planner import BLOCK_LOCATION_CPU, BlockPools
+
+    dev = torch.device("cuda:0")
+    _lib.load()
+    L, NB, H, D = 28, 16384, 4, 128
+    segs = kv_segments(torch, L, NB, H, D, torch.bfloat16, dev, 3)
+    S = len(segs)
+    tile = 16 * H * D * 2
+    page = S * tile
+    rng = np.random.default_rng(3)
+    tokens = np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, 64))), 16, 32768)
+    blocks = (np.ceil(tokens / 16)).astype(np.int64)
+    total = int(blocks.sum())
+    perm = rng.permutation(np.arange(1, NB))
+    out_ids = perm[:total]
+    in_ids = perm[total:2 * total]
+    if in_ids.size < total:
+        raise RuntimeError(f"{total} blocks per direction do not fit twice in {NB - 1} ids")
+    slab = 1 << 30
+    n_slabs = -(-total * page // slab) + 2
+    pools = BlockPools(n_slabs, slab)
+    host_ids = np.array(pools.allocate(total, BLOCK_LOCATION_CPU, (page // 2,)), np.int64)
+    pool = ops.PinnedHostPool(n_slabs * slab)
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    z = np.zeros(total, np.int32)
+    one = np.ones(total, np.int64)
+    res = {}
+    for mode in ("direct", "staged"):
+        for _ in range(args.warmup):
+            ops.swap_segments(segs, *common, out_ids, host_ids, z, z, one, False, mode=mode)
+            ops.swap_segments(segs, *common, host_ids, in_ids, z, z, one, True, mode=mode)
+        outs, ins = [], []
+        for _ in range(args.steps):
+            a, b = ev_pair(torch)
+            c, d = ev_pair(torch)
+            a.record()
+            ops.swap_segments(segs, *common, out_ids, host_ids, z, z, one, False, mode=mode)
+            b.record()
+            c.record()
+            ops.swap_segments(segs, *common, host_ids, in_ids, z, z, one, True, mode=mode)
+            d.record()
+            outs.append((a, b))
+            ins.append((c, d))
+        torch.cuda.synchronize()
+        t_out = statistics.median(x.elapsed_time(y) / 1e3 for x, y in outs)
+        t_in = statistics.median(x.elapsed_time(y) / 1e3 for x, y in ins)
+        di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
+        ok = all(torch.equal(t[di], t[do]) for t in segs)
+        if not ok:
+            raise AssertionError(f"varlen round trip not bit-exact ({mode})")
+        res[mode] = {"d2h_GBps": round(total * page / t_out / 1e9, 3),
+                     "h2d_GBps": round(total * page / t_in / 1e9, 3),
+                     "d2h_ms": round(t_out * 1e3, 3), "h2d_ms": round(t_in * 1e3, 3)}
+    link = measure_link(torch, ops, dev)
+    pool.free()
+    return {
+        "metric": "KV swap GB/s, variable-length batched swap",
+        "unit": "GB/s",
+        "config": {"workload": "Qwen2.5-7B KV 56 x [16384,16,4,128] bf16, 64 requests, "
+                               "log-normal lengths (median 1024, sigma 1.0), one call per direction",
+                   "blocks_per_direction": total, "bytes_per_direction": total * page,
+                   "host_ids": "slab allocator (contiguous runs)"},
+        "modes": res,
+        "link_GBps": {"d2h": round(link["d2h"], 3), "h2d": round(link["h2d"], 3)},
+        "bit_exact_round_trip": True,
+    }
+
+
+def bench_overlap(args):
+    """Qwen1.5-MoE KV shape (48 x [32768,16,16,128] bf16, 96 GiB): swap-out
+    of 16384 blocks, swap-in of 12288 blocks and copy_blocks of 2048 pairs,
+    each on its own stream, all enqueued together."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    _lib.load()
+    streams_raw = hip_streams(3)
+    bidir = measure_link_bidir(torch, ops, dev)
+    L, NB, H, D = 24, 32768, 16, 128
+    NOUT, NIN, NP = 16384, 12288, 2048
+    segs = kv_segments(torch, L, NB, H, D, torch.bfloat16, dev, 4)
+    S = len(segs)
+    tile = 16 * H * D * 2
+    page = S * tile
+    # 28,672 host pages need 84 GiB of pinned memory; hosts that cap pinned
+    # memory lower run the same shape with 3/4 of the swapped blocks.
+    scale = 1.0
+    try:
+        pool = ops.PinnedHostPool((NOUT + NIN) * page)
+    except _lib.AegkvError:
+        scale = 0.75
+        NOUT, NIN = int(NOUT * scale), int(NIN * scale)
+        pool = ops.PinnedHostPool((NOUT + NIN) * page)
+        log(f"pinned pool capped: running swap-out {NOUT}, swap-in {NIN} blocks")
+    rng = np.random.default_rng(4)
+    perm = rng.permutation(NB)
+    out_ids, in_ids = perm[:NOUT], perm[NOUT:NOUT + NIN]
+    csrc = perm[NOUT + NIN:NOUT + NIN + NP]
+    cdst = perm[NOUT + NIN + NP:NOUT + NIN + 2 * NP]
+    host_out = rng.permutation(NOUT + NIN)
+    host_x, host_y = host_out[:NOUT], host_out[NOUT:]
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    zo, oo = np.zeros(NOUT, np.int32), np.ones(NOUT, np.int64)
+    zi, oi = np.zeros(NIN, np.int32), np.ones(NIN, np.int64)
+    # the incoming model's blocks were swapped out earlier: put them on the
+    # host, remember their checksums, and clear them on the device
+    ops.swap_segments(segs, *common, in_ids, host_y, zi, zi, oi, False)
+    di = torch.from_numpy(in_ids).to(dev)
+    want_in = [t[di].view(NIN, -1).view(torch.int16).sum(dim=1, dtype=torch.int64) for t in segs]
+    for t in segs:
+        t.index_fill_(0, di, 0)
+    torch.cuda.synchronize()
+    # Three freshly created HIP streams (created before any other stream
+    # work of this run, so each gets its own hardware queue); three runs,
+    # the medians reported.
+    streams = [torch.cuda.ExternalStream(p) for p in streams_raw]
+    runs = []
+    for _ in range(3):
+        evs = [ev_pair(torch) for _ in range(3)]
+        begin = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        begin.record()
+        for st in streams:
+            st.wait_event(begin)
+        with torch.cuda.stream(streams[0]):
+            evs[0][0].record()
+            ops.swap_segments(segs, *common, out_ids, host_x, zo, zo, oo, False)
+            evs[0][1].record()
+        with torch.cuda.stream(streams[1]):
+            evs[1][0].record()
+            ops.swap_segments(segs, *common, host_y, in_ids, zi, zi, oi, True)
+            evs[1][1].record()
+        with torch.cuda.stream(streams[2]):
+            evs[2][0].record()
+            ops.copy_blocks(segs, csrc, cdst)
+            evs[2][1].record()
+        torch.cuda.synchronize()
+        runs.append((evs[0][0].elapsed_time(evs[0][1]) / 1e3,
+                     evs[1][0].elapsed_time(evs[1][1]) / 1e3,
+                     evs[2][0].elapsed_time(evs[2][1]) / 1e3,
+                     max(begin.elapsed_time(e[1]) for e in evs) / 1e3))
+    t_out, t_in, t_cp, span = (statistics.median(r[i] for r in runs) for i in range(4))
+    # correctness of everything that ran concurrently
+    ok_in = all(torch.equal(t[di].view(NIN, -1).view(torch.int16).sum(dim=1, dtype=torch.int64), w)
+                for t, w in zip(segs, want_in))
+    cs, cd = torch.from_numpy(csrc).to(dev), torch.from_numpy(cdst).to(dev)
+    ok_cp = all(torch.equal(t[cd], t[cs]) for t in segs)
+    pages = pool.tensor.view(NOUT + NIN, S, tile)
+    ok_out = all(torch.equal(pages[int(host_x[k]), s].to(dev),
+                             segs[s][int(out_ids[k])].view(torch.uint8).reshape(-1))
+                 for k in (0, NOUT // 2, NOUT - 1) for s in (0, S // 2, S - 1))
+    if not (ok_in and ok_cp and ok_out):
+        raise AssertionError(f"overlap check failed: in {ok_in} copy {ok_cp} out {ok_out}")
+    b_out, b_in, b_cp = NOUT * page, NIN * page, 2 * NP * page
+    pool.free()
+    return {
+        "metric": "KV swap + copy_blocks GB/s, three streams at once",
+        "unit": "GB/s",
+        "config": {"workload": f"Qwen1.5-MoE KV 48 x [32768,16,16,128] bf16; swap-out {NOUT}, "
+                               f"swap-in {NIN}, copy_blocks {NP} pairs, one stream each",
+                   "bytes": {"d2h": b_out, "h2d": b_in, "copy_rw": b_cp},
+                   "swap_block_scale": scale, "blocks": {"d2h": NOUT, "h2d": NIN, "pairs": NP}},
+        "d2h_GBps": round(b_out / t_out / 1e9, 3),
+        "h2d_GBps": round(b_in / t_in / 1e9, 3),
+        "copy_blocks_GBps": round(b_cp / t_cp / 1e9, 1),
+        "link_aggregate_GBps": round((b_out + b_in) / span / 1e9, 3),
+        "link_bidirectional_ceiling_GBps": round(bidir, 3),
+        "frac_bidirectional_ceiling": round((b_out + b_in) / span / 1e9 / bidir, 4),
+        "wall_ms": round(span * 1e3, 3),
+        "per_stream_ms": {"d2h": round(t_out * 1e3, 3), "h2d": round(t_in * 1e3, 3),
+                          "copy": round(t_cp * 1e3, 3)},
+        "runs": 3, "statistic": "median",
+        "bit_exact": True,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -161,6 +401,10 @@ def main():
               "(swaps shard per GPU with no exchange step; run one process per GPU).",
               file=sys.stderr)
         sys.exit(2)
+    if args.config != "headline":
+        fn = bench_varlen if args.config == "varlen" else bench_overlap
+        print(json.dumps(fn(args)), flush=True)
+        return
     import numpy as np
     import torch
 

@@ -51,7 +51,7 @@ extern "C" {
                                staging, plus SDMA hipMemcpyAsync of merged runs */
 
 /* tuning keys for aegkv_tune (values < 0 query without changing) */
-#define AEGKV_TUNE_WGS_PER_CU 1      /* persistent workgroups per CU      */
+#define AEGKV_TUNE_SWAP_OUT_WORKGROUPS 1 /* swap-out kernel: workgroups    */
 #define AEGKV_TUNE_STAGING_BYTES 2   /* max device staging per chunk      */
 #define AEGKV_TUNE_AUTO_D2H 3        /* mode AUTO picks for swap-out      */
 #define AEGKV_TUNE_AUTO_H2D 4        /* mode AUTO picks for swap-in       */
@@ -62,6 +62,7 @@ extern "C" {
                                         the page size, else 1-6, 8 or 10   */
 #define AEGKV_TUNE_SWAP_SHAPE_AUTO 8 /* 1: swap kernels pick their shape
                                         from the page size like copy_blocks */
+#define AEGKV_TUNE_SWAP_IN_WORKGROUPS 9 /* swap-in kernel: workgroups      */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -183,7 +183,7 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
 @pytest.fixture
 def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
-            _lib.TUNE_WGS_PER_CU, _lib.TUNE_NT_STORES)
+            _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -212,10 +212,11 @@ def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
 
 
 @pytest.mark.parametrize("shape_auto", [0, 1])
-@pytest.mark.parametrize("wpc", [1, 8, 64])
+@pytest.mark.parametrize("wpc", [1, 37, 4096])
 def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, wpc):
     _lib.tune(_lib.TUNE_SWAP_SHAPE_AUTO, shape_auto)
-    _lib.tune(_lib.TUNE_WGS_PER_CU, wpc)
+    _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS, wpc)
+    _lib.tune(_lib.TUNE_SWAP_IN_WORKGROUPS, wpc)
     rng = np.random.default_rng(31 + wpc)
     page = np.array([160 * 1024, 32 * 1024, 4096, 48 * 1024 + 16 * 4], np.int64)
     cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)

@@ -241,10 +241,10 @@ def test_early_validation_without_gpu(aegkv_lib):
 def test_tuning_knobs(aegkv_lib):
     from aegaeon_amd import _lib
 
-    prev = _lib.tune(_lib.TUNE_WGS_PER_CU)
+    prev = _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS)
     assert prev >= 1
-    assert _lib.tune(_lib.TUNE_WGS_PER_CU, 4) == prev
-    assert _lib.tune(_lib.TUNE_WGS_PER_CU, prev) == 4
+    assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS, 4) == prev
+    assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS, prev) == 4
     assert _lib.tune(_lib.TUNE_AUTO_D2H) in (_lib.MODE_DIRECT, _lib.MODE_STAGED)
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_AUTO_D2H, 7)
