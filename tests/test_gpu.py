@@ -506,3 +506,90 @@ def test_llama2_13b_copy_blocks_full_size(gpu):
         assert torch.equal(s[dd], s[ds]), i
         after = s.view(8192, -1).view(torch.int16).sum(dim=1, dtype=torch.int64)
         assert torch.equal(after[keep], sums[i][keep]), i
+
+
+def test_qwen25_7b_varlen_batched_round_trip(gpu):
+    """56 x [16384,16,4,128] bf16; 64 requests with log-normal lengths,
+    blocks at seeded random device ids, host ids from the slab allocator;
+    one batched call per direction in each mode, bit-exact round trip."""
+    from aegaeon_amd.planner import BLOCK_LOCATION_CPU, BlockPools
+
+    _say("Qwen2.5-7B variable-length batched round trip")
+    segs = _kv_segments(28, 16384, 4, 128, torch.bfloat16, gpu, 3)
+    S, tile = len(segs), 16 * 4 * 128 * 2
+    page = S * tile
+    rng = np.random.default_rng(30)
+    tokens = np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, 64))), 16, 32768)
+    total = int(np.ceil(tokens / 16).sum())
+    perm = rng.permutation(np.arange(1, 16384))
+    assert 2 * total <= perm.size
+    out_ids, in_ids = perm[:total], perm[total:2 * total]
+    slab = 1 << 30
+    n_slabs = -(-total * page // slab) + 1
+    pools = BlockPools(n_slabs, slab)
+    host_ids = np.array(pools.allocate(total, BLOCK_LOCATION_CPU, (page // 2,)), np.int64)
+    pool = ops.PinnedHostPool(n_slabs * slab)
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, 16384, [1], pool.tensor, page, 0)
+    z, one = np.zeros(total, np.int32), np.ones(total, np.int64)
+    di, do = torch.from_numpy(in_ids).to(gpu), torch.from_numpy(out_ids).to(gpu)
+    for mode in MODES:
+        for t in segs:
+            t.index_fill_(0, di, 0)
+        ops.swap_segments(segs, *common, out_ids, host_ids, z, z, one, False, mode=mode)
+        ops.swap_segments(segs, *common, host_ids, in_ids, z, z, one, True, mode=mode)
+        torch.cuda.synchronize()
+        for s in range(S):
+            assert torch.equal(segs[s][di], segs[s][do]), (mode, s)
+    pool.free()
+
+
+def test_three_stream_overlap_correctness(gpu):
+    """Qwen1.5-MoE tile shape (48 x 64 KiB), scaled to 4096 blocks: swap-out,
+    swap-in and copy_blocks enqueued together on three streams must each be
+    exact."""
+    _say("three-stream overlap")
+    NB, NOUT, NIN, NP = 4096, 1024, 768, 512
+    segs = _kv_segments(24, NB, 16, 128, torch.bfloat16, gpu, 4)
+    S, tile = len(segs), 16 * 16 * 128 * 2
+    page = S * tile
+    rng = np.random.default_rng(40)
+    perm = rng.permutation(NB)
+    out_ids, in_ids = perm[:NOUT], perm[NOUT:NOUT + NIN]
+    csrc = perm[NOUT + NIN:NOUT + NIN + NP]
+    cdst = perm[NOUT + NIN + NP:NOUT + NIN + 2 * NP]
+    pool = ops.PinnedHostPool((NOUT + NIN) * page)
+    hp = rng.permutation(NOUT + NIN)
+    hx, hy = hp[:NOUT], hp[NOUT:]
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    zo, oo = np.zeros(NOUT, np.int32), np.ones(NOUT, np.int64)
+    zi, oi = np.zeros(NIN, np.int32), np.ones(NIN, np.int64)
+    ops.swap_segments(segs, *common, in_ids, hy, zi, zi, oi, False)
+    di = torch.from_numpy(in_ids).to(gpu)
+    want_in = [t[di].clone() for t in segs]
+    for t in segs:
+        t.index_fill_(0, di, 0)
+    want_cp = [t[torch.from_numpy(csrc).to(gpu)].clone() for t in segs]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    begin = torch.cuda.Event()
+    begin.record()
+    for st in streams:
+        st.wait_event(begin)
+    with torch.cuda.stream(streams[0]):
+        ops.swap_segments(segs, *common, out_ids, hx, zo, zo, oo, False)
+    with torch.cuda.stream(streams[1]):
+        ops.swap_segments(segs, *common, hy, in_ids, zi, zi, oi, True)
+    with torch.cuda.stream(streams[2]):
+        ops.copy_blocks(segs, csrc, cdst)
+    torch.cuda.synchronize()
+    dcd = torch.from_numpy(cdst).to(gpu)
+    pages = pool.tensor.view(NOUT + NIN, S, tile)
+    for s in range(S):
+        assert torch.equal(segs[s][di], want_in[s]), s
+        assert torch.equal(segs[s][dcd], want_cp[s]), s
+    hxt = torch.from_numpy(hx)
+    for s in (0, S // 2, S - 1):
+        got = pages[hxt, s].to(gpu)
+        want = segs[s][torch.from_numpy(out_ids).to(gpu)].view(NOUT, -1).view(torch.uint8)
+        assert torch.equal(got, want), s
+    pool.free()
