@@ -51,10 +51,13 @@ def parse():
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
-    p.add_argument("--config", default="headline", choices=["headline", "varlen", "overlap"],
+    p.add_argument("--config", default="headline",
+                   choices=["headline", "varlen", "overlap", "refplan"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
                         "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
-                        "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams")
+                        "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams; "
+                        "refplan: the reference benchmark's extent plans, libaegkv beside "
+                        "the reference's per-extent copy_ loop on the same GPU")
     return p.parse_args()
 
 
@@ -394,6 +397,99 @@ def bench_overlap(args):
     }
 
 
+def bench_refplan(args):
+    """The extent plans of benchmark/benchmark_composite_swap.py:35-64 with
+    its defaults (:119-133): 8 segments of a 17,301,504-byte physical page,
+    528-token physical pages, 16-token kernel blocks, 3 fixed pages, lengths
+    1..1057. Each plan moves page i of the host pool to/from page i of every
+    segment, either whole ("full") or only the live kernel blocks
+    ("optimized"). Timed: libaegkv (one launch per call) and the reference's
+    own per-extent copy_(non_blocking=True) loop (aegaeon/worker.py:2272-2328,
+    restated in the oracle) on the same GPU and stream; p50 of `--steps`
+    iterations after `--warmup`."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+    from aegaeon_amd.cache_transfer import kernel_block_extent_for_attention_page
+    from oracle import oracle
+
+    dev = torch.device("cuda:0")
+    _lib.load()
+    seg_n, phys_bytes, phys_tok, kern_tok, fixed = 8, 17_301_504, 528, 16, 3
+    seg_page = phys_bytes // seg_n
+    kpp = phys_tok // kern_tok
+    stream = torch.cuda.Stream()
+    out = []
+
+    def p50(fn):
+        for _ in range(args.warmup):
+            with torch.cuda.stream(stream):
+                fn()
+        samples = []
+        for _ in range(args.steps):
+            a, b = ev_pair(torch)
+            with torch.cuda.stream(stream):
+                a.record(stream)
+                fn()
+                b.record(stream)
+            b.synchronize()
+            samples.append(a.elapsed_time(b))
+        return statistics.median(samples)
+
+    for length in (1, 128, 256, 512, 528, 529, 1057):
+        pages = fixed + math.ceil(length / phys_tok)
+        plans = {"full": [(0, kpp)] * pages,
+                 "optimized": [(0, kpp)] * fixed + [
+                     kernel_block_extent_for_attention_page(length, b, phys_tok, kern_tok)
+                     for b in range(pages - fixed)]}
+        host = ops.PinnedHostPool(pages * phys_bytes)
+        segs = [torch.empty(pages, seg_page, dtype=torch.uint8, device=dev) for _ in range(seg_n)]
+        for t in segs:
+            t.random_(0, 256)
+        ids = np.arange(pages)
+        host_view = host.tensor.view(pages, phys_bytes)
+        row = {"length": length, "pages": pages}
+        for name, plan in plans.items():
+            first = np.array([f for f, _ in plan], np.int64)
+            valid = np.array([c for _, c in plan], np.int64)
+            grp = np.zeros(pages, np.int32)
+            moved = int(valid.sum()) * (seg_page // kpp) * seg_n
+            row[f"{name}_bytes"] = moved
+            for direction, is_in in (("H2D", True), ("D2H", False)):
+                t_aeg = p50(lambda: ops.swap_segments(
+                    segs, [seg_page] * seg_n, [s * seg_page for s in range(seg_n)],
+                    [1] * seg_n, pages, [kpp], host.tensor, phys_bytes, 0, ids, ids, grp,
+                    first, valid, is_in))
+                t_ref = p50(lambda: oracle.swap_blocks_torch(
+                    segs, host_view, [s * seg_page for s in range(seg_n)], [{0}] * seg_n,
+                    [kpp], 0, phys_bytes, ids, ids, grp, first, valid, is_in,
+                    non_blocking=True))
+                row[f"{name}_{direction}_ms"] = {"aegkv": round(t_aeg, 4),
+                                                 "reference_loop": round(t_ref, 4)}
+        # the last plan run both ways: check it landed where the plan says
+        torch.cuda.synchronize()
+        for s in range(seg_n):
+            for pg, (f, c) in enumerate(plans["optimized"]):
+                lo, hi = f * (seg_page // kpp), (f + c) * (seg_page // kpp)
+                if hi > lo and not torch.equal(
+                        segs[s][pg, lo:hi].cpu(),
+                        host_view[pg, s * seg_page + lo:s * seg_page + hi]):
+                    raise AssertionError(f"refplan mismatch at length {length}")
+        out.append(row)
+        del segs
+        host.free()
+    return {
+        "metric": "reference benchmark extent plans: p50 ms per call",
+        "config": {"workload": "benchmark_composite_swap defaults: 8 segments, 17,301,504-byte "
+                               "physical page, 528-token pages, 16-token kernel blocks, 3 fixed "
+                               "pages", "warmup": args.warmup, "iters": args.steps},
+        "rows": out,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -402,7 +498,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.config != "headline":
-        fn = bench_varlen if args.config == "varlen" else bench_overlap
+        fn = {"varlen": bench_varlen, "overlap": bench_overlap,
+              "refplan": bench_refplan}[args.config]
         print(json.dumps(fn(args)), flush=True)
         return
     import numpy as np

@@ -213,14 +213,16 @@ def copy_blocks(segments: Sequence[np.ndarray], segment_page_bytes, num_blocks: 
 
 def swap_blocks_torch(gpu_pages, host_view, segment_cpu_offsets, segment_owners,
                       group_kernel_blocks_per_page, tp_rank: int, composite_page_bytes: int,
-                      src_ids, dst_ids, group_ids, first, valid, is_swap_in: bool):
+                      src_ids, dst_ids, group_ids, first, valid, is_swap_in: bool,
+                      non_blocking: bool = False):
     """The reference's torch path, aegaeon/worker.py:2272-2328, on host tensors.
 
     gpu_pages[s] is backing tensor s viewed as uint8 [num_blocks, page_s]
     (worker.py:2273-2277); host_view is uint8 [num_host_blocks, host_page]
     (worker.py:1428-1432). One narrow(...).copy_() per (segment, entry)
     extent, segment-outer, exactly as the reference issues them (without
-    non_blocking, which has no effect between host tensors).
+    non_blocking, which has no effect between host tensors; pass
+    non_blocking=True for device tensors, as the reference does).
     """
     copied = 0
     ops = 0
@@ -238,9 +240,11 @@ def swap_blocks_torch(gpu_pages, host_view, segment_cpu_offsets, segment_owners,
             ops += 1
             hoff = tp_rank * composite_page_bytes + segment_cpu_offsets[s] + off
             if is_swap_in:
-                pages[dst].narrow(0, off, ln).copy_(host_view[src].narrow(0, hoff, ln))
+                pages[dst].narrow(0, off, ln).copy_(host_view[src].narrow(0, hoff, ln),
+                                                    non_blocking=non_blocking)
             else:
-                host_view[dst].narrow(0, hoff, ln).copy_(pages[src].narrow(0, off, ln))
+                host_view[dst].narrow(0, hoff, ln).copy_(pages[src].narrow(0, off, ln),
+                                                         non_blocking=non_blocking)
     return copied, ops
 
 
