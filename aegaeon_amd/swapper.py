@@ -7,16 +7,20 @@ wait_for_all_move_in/out (:2406-2418). The reference issues one
 torch copy_ per (segment, entry) extent from a Python double loop; here the
 whole list is one call into libaegkv.so, one kernel launch per call.
 
-Cross-process plumbing (Ray object refs, CUDA IPC event handles) is not part
-of this module: source events are local torch.cuda.Event objects and the
-returned completion event is a local event.
+A source event may be a local torch.cuda.Event or the IPC handle bytes
+another process exported (utils.py:263-288 reduce/rebuild_cuda_event). With
+interprocess_events=True the completion events are created interprocess-capable
+like the reference's (worker.py:2249) and event_ipc_handle() exports them;
+the default is local events, because the HIP runtime used here rejects
+recording interprocess events (hipErrorInvalidValue). Ray object refs are not
+part of this module.
 """
 
 from __future__ import annotations
 
 import logging
 from collections import defaultdict
-from typing import Dict, List, Optional, Sequence
+from typing import Dict, List, Optional, Sequence, Union
 
 import numpy as np
 import torch
@@ -34,7 +38,7 @@ class KVSwapper:
     def __init__(self, cache: CompositeCache, group_layer_names: Sequence[set],
                  group_descriptors: Sequence[CacheGroupRuntimeConfig],
                  host_pool: torch.Tensor, tp_rank: int = 0, tp_size: int = 1,
-                 host_element_size: int = 2):
+                 host_element_size: int = 2, interprocess_events: bool = False):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -42,6 +46,7 @@ class KVSwapper:
         if not 0 <= tp_rank < tp_size:
             raise ValueError(f"tp_rank {tp_rank} outside [0, {tp_size})")
         self.cache = cache
+        self.interprocess_events = interprocess_events
         self.group_descriptors = list(group_descriptors)
         self.tp_rank = tp_rank
         self.tp_size = tp_size
@@ -94,8 +99,8 @@ class KVSwapper:
     def swap_blocks(self, request_ids: Sequence[int], source_block_ids: Sequence[int],
                     target_block_ids: Sequence[int], group_ids: Sequence[int],
                     first_kernel_blocks: Sequence[int], valid_kernel_blocks: Sequence[int],
-                    source_events: Sequence[Optional[torch.cuda.Event]], is_swap_in: bool,
-                    mode="auto") -> torch.cuda.Event:
+                    source_events: Sequence[Optional[Union[torch.cuda.Event, bytes]]],
+                    is_swap_in: bool, mode="auto") -> torch.cuda.Event:
         """Move the live extents of some blocks between host and device.
 
         is_swap_in: host block source_block_ids[i] -> device block
@@ -120,10 +125,13 @@ class KVSwapper:
         if len(source_events) != len(request_ids):
             raise ValueError("one source event slot per request is required")
         stream = self.swap_in_stream if is_swap_in else self.swap_out_stream
-        new_event = torch.cuda.Event()
-        # wait for in-flight moves of the same requests (worker.py:2351-2394)
+        new_event = torch.cuda.Event(interprocess=self.interprocess_events)
+        # wait for in-flight moves of the same requests (worker.py:2351-2394);
+        # bytes are IPC handles exported by another process
         for rid, ev in zip(request_ids, source_events):
             if ev is not None:
+                if isinstance(ev, (bytes, bytearray)):
+                    ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
                 stream.wait_event(ev)
             self.move_event_table[rid].append(new_event)
         ops.swap_segments(
@@ -145,6 +153,12 @@ class KVSwapper:
                         "CPU" if is_swap_in else "GPU", "GPU" if is_swap_in else "CPU",
                         copied, full, saved * 100, extents)
         return new_event
+
+    @staticmethod
+    def event_ipc_handle(event: torch.cuda.Event) -> bytes:
+        """IPC handle of a swap's completion event, for another process to
+        open with torch.cuda.Event.from_ipc_handle (worker.py:2349)."""
+        return event.ipc_handle()
 
     def clear_request_resource(self, request_id: int) -> None:
         self.move_event_table.pop(request_id, None)

@@ -397,6 +397,34 @@ def bench_overlap(args):
     }
 
 
+def reference_submit_copies(cpu_pages, gpu_segments, extents, is_swap_in):
+    """The reference benchmark's copy loop (benchmark_composite_swap.py:67-87):
+    one narrow().copy_(non_blocking=True) per (segment, page) extent."""
+    seg_page = gpu_segments[0].shape[1]
+    for s, gpu_pages in enumerate(gpu_segments):
+        for page_id, (off, ln) in enumerate(extents):
+            if ln == 0:
+                continue
+            cpu_ext = cpu_pages[page_id].narrow(0, s * seg_page + off, ln)
+            gpu_ext = gpu_pages[page_id].narrow(0, off, ln)
+            if is_swap_in:
+                gpu_ext.copy_(cpu_ext, non_blocking=True)
+            else:
+                cpu_ext.copy_(gpu_ext, non_blocking=True)
+
+
+def reference_worker_loop(gpu_pages, host_view, tile, src_ids, dst_ids, is_swap_in):
+    """Worker.swap_blocks' copy loop (aegaeon/worker.py:2272-2328) for whole
+    tiles: segment-outer, entry-inner, one copy_(non_blocking=True) each."""
+    for s, pages in enumerate(gpu_pages):
+        hoff = s * tile
+        for src, dst in zip(src_ids, dst_ids):
+            if is_swap_in:
+                pages[dst].copy_(host_view[src].narrow(0, hoff, tile), non_blocking=True)
+            else:
+                host_view[dst].narrow(0, hoff, tile).copy_(pages[src], non_blocking=True)
+
+
 def bench_refplan(args):
     """The extent plans of benchmark/benchmark_composite_swap.py:35-64 with
     its defaults (:119-133): 8 segments of a 17,301,504-byte physical page,
@@ -404,17 +432,17 @@ def bench_refplan(args):
     1..1057. Each plan moves page i of the host pool to/from page i of every
     segment, either whole ("full") or only the live kernel blocks
     ("optimized"). Timed: libaegkv (one launch per call) and the reference's
-    own per-extent copy_(non_blocking=True) loop (aegaeon/worker.py:2272-2328,
-    restated in the oracle) on the same GPU and stream; p50 of `--steps`
-    iterations after `--warmup`."""
+    own per-extent copy_(non_blocking=True) loop (submit_copies,
+    benchmark_composite_swap.py:67-87, restated below) on the same GPU and
+    stream; p50 of `--steps` iterations after `--warmup`."""
     import math
 
     import numpy as np
     import torch
 
     from aegaeon_amd import _lib, ops
-    from aegaeon_amd.cache_transfer import kernel_block_extent_for_attention_page
-    from oracle import oracle
+    from aegaeon_amd.cache_transfer import (byte_extent_for_kernel_blocks,
+                                            kernel_block_extent_for_attention_page)
 
     dev = torch.device("cuda:0")
     _lib.load()
@@ -463,10 +491,8 @@ def bench_refplan(args):
                     segs, [seg_page] * seg_n, [s * seg_page for s in range(seg_n)],
                     [1] * seg_n, pages, [kpp], host.tensor, phys_bytes, 0, ids, ids, grp,
                     first, valid, is_in))
-                t_ref = p50(lambda: oracle.swap_blocks_torch(
-                    segs, host_view, [s * seg_page for s in range(seg_n)], [{0}] * seg_n,
-                    [kpp], 0, phys_bytes, ids, ids, grp, first, valid, is_in,
-                    non_blocking=True))
+                extents = [byte_extent_for_kernel_blocks(seg_page, kpp, f, c) for f, c in plan]
+                t_ref = p50(lambda: reference_submit_copies(host_view, segs, extents, is_in))
                 row[f"{name}_{direction}_ms"] = {"aegkv": round(t_aeg, 4),
                                                  "reference_loop": round(t_ref, 4)}
         # the last plan run both ways: check it landed where the plan says
@@ -481,12 +507,45 @@ def bench_refplan(args):
         out.append(row)
         del segs
         host.free()
+
+    # Qwen3-4B: 1024 scattered blocks each way, whole tiles.
+    S1, NB1, tile1, HOST1, n = 72, 8192, 32768, 4096, 1024
+    segs1 = kv_segments(torch, 36, NB1, 8, 128, torch.bfloat16, dev, 1)
+    pages1 = [t.view(torch.uint8).view(NB1, tile1) for t in segs1]
+    pool = ops.PinnedHostPool(HOST1 * S1 * tile1)
+    hv = pool.tensor.view(HOST1, S1 * tile1)
+    g = torch.Generator().manual_seed(1)
+    out_ids = (torch.randperm(NB1 - 1, generator=g)[:n] + 1).numpy()
+    host_ids = torch.randperm(HOST1, generator=g)[:n].numpy()
+    rest = np.setdiff1d(np.arange(1, NB1), out_ids)
+    in_ids = rest[torch.randperm(rest.size, generator=g)[:n].numpy()]
+    common = ([tile1] * S1, [i * tile1 for i in range(S1)], [1] * S1, NB1, [1], pool.tensor,
+              S1 * tile1, 0)
+    z, one = np.zeros(n, np.int32), np.ones(n, np.int64)
+    t_out = p50(lambda: ops.swap_segments(segs1, *common, out_ids, host_ids, z, z, one, False))
+    t_in = p50(lambda: ops.swap_segments(segs1, *common, host_ids, in_ids, z, z, one, True))
+    pl_out, pl_h, pl_in = out_ids.tolist(), host_ids.tolist(), in_ids.tolist()
+    r_out = p50(lambda: reference_worker_loop(pages1, hv, tile1, pl_out, pl_h, False))
+    r_in = p50(lambda: reference_worker_loop(pages1, hv, tile1, pl_h, pl_in, True))
+    torch.cuda.synchronize()
+    di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
+    if not all(torch.equal(t[di], t[do]) for t in segs1):
+        raise AssertionError("Qwen3-4B reference-loop round trip not bit-exact")
+    b1 = n * S1 * tile1
+    qwen = {"blocks": n, "extents_per_direction": n * S1, "bytes_per_direction": b1,
+            "aegkv_ms": {"D2H": round(t_out, 3), "H2D": round(t_in, 3)},
+            "reference_loop_ms": {"D2H": round(r_out, 3), "H2D": round(r_in, 3)},
+            "aegkv_GBps": {"D2H": round(b1 / t_out / 1e6, 2), "H2D": round(b1 / t_in / 1e6, 2)},
+            "reference_loop_GBps": {"D2H": round(b1 / r_out / 1e6, 2),
+                                    "H2D": round(b1 / r_in / 1e6, 2)}}
+    pool.free()
     return {
         "metric": "reference benchmark extent plans: p50 ms per call",
         "config": {"workload": "benchmark_composite_swap defaults: 8 segments, 17,301,504-byte "
                                "physical page, 528-token pages, 16-token kernel blocks, 3 fixed "
                                "pages", "warmup": args.warmup, "iters": args.steps},
         "rows": out,
+        "qwen3_4b_1024_blocks": qwen,
     }
 
 
@@ -658,6 +717,30 @@ def main():
             "avg_launch_ms_d2h": round(t_d2h * 1e3, 3),
             "avg_launch_ms_h2d": round(t_h2d * 1e3, 3),
         },
+    }
+    # The reference's own data path on this GPU: Worker.swap_blocks' loop of
+    # one copy_(non_blocking=True) per (segment, block) tile, same blocks.
+    log("timing the reference per-extent copy loop on the same GPU")
+    pages1 = [t.view(torch.uint8).view(NB1, tile1) for t in segs1]
+    hv = pool.tensor.view(HOST1, S1 * tile1)
+    ref = {}
+    for name, src_l, dst_l, is_in in (("d2h", out_ids.tolist(), host_ids.tolist(), False),
+                                      ("h2d", host_ids.tolist(), in_ids.tolist(), True)):
+        reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)  # warm-up
+        a, b = ev_pair(torch)
+        a.record()
+        reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)
+        b.record()
+        b.synchronize()
+        ref[name] = swap_bytes / (a.elapsed_time(b) / 1e3) / 1e9
+    if not all(torch.equal(s[di], s[do]) for s in segs1):
+        raise AssertionError("reference-loop round trip is not bit-exact")
+    line["reference_path_same_gpu"] = {
+        "what": "reference per-extent copy_ loop (aegaeon/worker.py:2272-2328), 73,728 "
+                "copies per direction, same blocks and pool",
+        "d2h_GBps": round(ref["d2h"], 3), "h2d_GBps": round(ref["h2d"], 3),
+        "speedup_d2h": round(d2h_gbps / ref["d2h"], 2),
+        "speedup_h2d": round(h2d_gbps / ref["h2d"], 2),
     }
     pool.free()
     del segs1, segs2

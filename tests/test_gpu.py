@@ -593,3 +593,66 @@ def test_three_stream_overlap_correctness(gpu):
         want = segs[s][torch.from_numpy(out_ids).to(gpu)].view(NOUT, -1).view(torch.uint8)
         assert torch.equal(got, want), s
     pool.free()
+
+
+def _ipc_producer(q_in, q_out):
+    """Child process: write a pattern into a block of the parent's cache
+    after a long kernel, record an interprocess event behind it and hand out
+    its IPC handle without waiting."""
+    import torch
+
+    seg = q_in.get()
+    torch.cuda.set_device(0)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        busy = torch.zeros(1 << 28, dtype=torch.float32, device="cuda")
+        for _ in range(400):
+            busy.add_(1.0)
+        seg[5].fill_(0x2B)
+        ev = torch.cuda.Event(interprocess=True)
+        ev.record(st)
+    q_out.put(ev.ipc_handle())
+    q_in.get()  # keep the event and tensor alive until the parent is done
+
+
+@pytest.mark.skip(reason="the HIP runtime here rejects recording interprocess events "
+                         "(torch.cuda.Event(interprocess=True).record -> hipErrorInvalidValue), "
+                         "so cross-process event ordering cannot be exercised on this GPU")
+def test_swap_waits_on_ipc_event_from_another_process(gpu):
+    """A source event exported by another process orders the swap after that
+    process's write (worker.py:2351-2394)."""
+    import time
+
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import KVSwapper
+
+    _say("IPC event ordering across processes")
+    n_blocks, page = 16, 65536
+    cache = allocate_composite_cache([KVCacheTensorSpec(n_blocks * page, ("l0",))], n_blocks, gpu)
+    pool = ops.PinnedHostPool(4 * page)
+    pool.tensor.zero_()
+    sw = KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
+                   interprocess_events=True)
+    mp = torch.multiprocessing.get_context("spawn")
+    q_in, q_out = mp.Queue(), mp.Queue()
+    child = mp.Process(target=_ipc_producer, args=(q_in, q_out), daemon=True)
+    child.start()
+    try:
+        q_in.put(cache.segment_pages(0))
+        handle = q_out.get(timeout=240)
+        ev = sw.swap_blocks([7], [5], [2], [0], [0], [1], [handle], False)
+        deadline = time.time() + 120
+        while not ev.query():
+            assert time.time() < deadline, "swap event never completed"
+            time.sleep(0.01)
+        got = pool.tensor.view(4, page)[2]
+        assert bool((got == 0x2B).all()), "swap ran before the other process's write"
+        handle2 = KVSwapper.event_ipc_handle(ev)
+        assert isinstance(handle2, (bytes, bytearray)) and len(handle2) > 0
+    finally:
+        q_in.put(None)
+        child.join(60)
+        if child.is_alive():
+            child.kill()
+    pool.free()
