@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_swap",
     "aegkv_swap_blocks",
     "aegkv_copy_blocks",
+    "aegkv_transfer_entries",
     "aegkv_host_alloc",
     "aegkv_host_free",
 )
@@ -73,6 +74,11 @@ _SIGNATURES = {
          _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P],
     ),
     "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_transfer_entries": (
+        _INT,
+        [_I32, _I32P, _I64P, _I64P, _I64P, _I64, _I64P, _I64P, _I64P, _I64, _I64P, _I32P,
+         _I64P, _I64P, _I64P, _I64P, _I64P],
+    ),
     "aegkv_host_alloc": (_INT, [_PP, _I64]),
     "aegkv_host_free": (_INT, [_P]),
 }

@@ -25,6 +25,7 @@
 
 #include <hip/hip_runtime.h>
 #include "aegkv.h"
+#include "errors.h"
 
 #include <algorithm>
 #include <cstdarg>
@@ -35,19 +36,25 @@
 #include <mutex>
 #include <vector>
 
-namespace {
-
 // ---------------------------------------------------------------- errors --
 
+namespace {
 thread_local char g_err[512] = "";
+}  // namespace
 
-int fail(int code, const char* fmt, ...) {
+int aegkv_set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
   vsnprintf(g_err, sizeof(g_err), fmt, ap);
   va_end(ap);
   return code;
 }
+
+void aegkv_clear_error() { g_err[0] = '\0'; }
+
+namespace {
+
+#define fail aegkv_set_error
 
 int hip_fail(hipError_t e, const char* what) {
   return fail(static_cast<int>(e), "%s failed: %s (%d)", what, hipGetErrorString(e),

@@ -11,11 +11,15 @@ ABI) and calls BlockPools.reclaim(plan) once the move's event has completed.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from collections import defaultdict, deque
 from dataclasses import dataclass, field
 from typing import Deque, Dict, List, Optional, Sequence, Tuple
 
+import numpy as np
+
+from . import _lib
 from .cache_groups import (
     BLOCK_LOCATION_CPU,
     VLLM_NULL_BLOCK_ID,
@@ -140,6 +144,50 @@ class BlockPools:
         self.release(plan.release_source_block_ids, plan.source_location, plan.block_shape)
 
 
+_KIND = {"attention": 0, "mamba_none": 1}
+
+
+def native_transfer_entries(groups: Sequence[CacheGroupConfig],
+                            tables: Sequence[Tuple[BlockTable, int]]
+                            ) -> List[List[Tuple[int, int, int, int, int]]]:
+    """BlockTable.transfer_entries for many tables sharing `groups`, in one
+    call into libaegkv (aegkv_transfer_entries). Returns one row list per
+    table, each row (group, column, block id, first, count)."""
+    n_groups = len(groups)
+    kind = np.array([_KIND[g.kind] for g in groups], np.int32)
+    bs = np.array([g.block_size for g in groups], np.int64)
+    kbs = np.array([g.kernel_block_size for g in groups], np.int64)
+    win = np.array([0 if g.sliding_window is None else g.sliding_window for g in groups],
+                   np.int64)
+    tokens = np.array([tok for _, tok in tables], np.int64)
+    lengths = [len(col) for table, _ in tables for col in table.group_blocks]
+    if any(len(table.group_blocks) != n_groups for table, _ in tables):
+        raise ValueError("every table must have one column list per cache group")
+    offsets = np.zeros(len(lengths) + 1, np.int64)
+    np.cumsum(lengths, out=offsets[1:])
+    ids = np.fromiter((b for table, _ in tables for col in table.group_blocks for b in col),
+                      dtype=np.int64, count=int(offsets[-1]))
+    cap = max(1, int(offsets[-1]))
+    out = {name: np.empty(cap, np.int64) for name in ("table", "column", "block", "first",
+                                                       "count")}
+    out_group = np.empty(cap, np.int32)
+    n = ctypes.c_int64()
+    p64 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))  # noqa: E731
+    rc = _lib.load().aegkv_transfer_entries(
+        n_groups, kind.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), p64(bs), p64(kbs),
+        p64(win), len(tables), p64(tokens), p64(offsets), p64(ids), cap, p64(out["table"]),
+        out_group.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), p64(out["column"]),
+        p64(out["block"]), p64(out["first"]), p64(out["count"]), ctypes.byref(n))
+    _lib.check(rc)
+    m = n.value
+    rows: List[List[Tuple[int, int, int, int, int]]] = [[] for _ in tables]
+    cols = zip(out["table"][:m].tolist(), out_group[:m].tolist(), out["column"][:m].tolist(),
+               out["block"][:m].tolist(), out["first"][:m].tolist(), out["count"][:m].tolist())
+    for t, g, c, b, f, k in cols:
+        rows[t].append((g, c, b, f, k))
+    return rows
+
+
 @dataclass
 class SwapPlan:
     """One swap_blocks call's lists plus the bookkeeping of the move."""
@@ -207,12 +255,18 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
                 raise ValueError(
                     f"request {rid} cache groups do not match target engine #{target_location}"
                 )
-        entries = table.transfer_entries(tokens)
-        plans.append((table, tokens, entries))
+        plans.append((table, tokens, None))
         moved_ids.append(rid)
         release += table.blocks
     if not plans:
         return None
+    # every moved table shares the source's cache groups; plan them in one call
+    groups = plans[0][0].cache_groups
+    if all(tuple(t.cache_groups) == tuple(groups) for t, _, _ in plans):
+        native = native_transfer_entries(groups, [(t, tok) for t, tok, _ in plans])
+        plans = [(t, tok, rows) for (t, tok, _), rows in zip(plans, native)]
+    else:
+        plans = [(t, tok, t.transfer_entries(tok)) for t, tok, _ in plans]
     targets = pools.allocate(sum(len(e) for _, _, e in plans), target_location, shape)
     plan = SwapPlan(moved_ids, src_loc, target_location, shape,
                     release_source_block_ids=release)
@@ -221,14 +275,18 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
     for table, tokens, entries in plans:
         mine = targets[cursor:cursor + len(entries)]
         cursor += len(entries)
-        for (g, _, pid, first, count), tid in zip(entries, mine):
+        # destination table: retained columns get their new ids, everything
+        # else stays released (BlockTable.moved_group_blocks, same rows)
+        moved = [[-1] * len(col) for col in table.group_blocks]
+        for (g, col, pid, first, count), tid in zip(entries, mine):
+            moved[g][col] = tid
             if count > 0:
                 plan.source_block_ids.append(pid)
                 plan.target_block_ids.append(tid)
                 plan.group_ids.append(g)
                 plan.first_kernel_blocks.append(first)
                 plan.valid_kernel_blocks.append(count)
-        new_tables.append(table.moved_group_blocks(tokens, mine))
+        new_tables.append(moved)
     for (table, _, _), groups in zip(plans, new_tables):
         table.group_blocks = groups
         table.location = target_location

@@ -147,6 +147,34 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
                       const int64_t* dst_block_ids, hipStream_t stream);
 
 /*
+ * Transfer entries of many block tables in one call (host-only; no GPU).
+ * Native form of BlockTable.transfer_entries (aegaeon/block_manager.py:
+ * 446-478) over CacheGroupConfig.num_skipped_blocks / kernel_block_extent
+ * (:196-266) and kernel_block_extent_for_attention_page
+ * (aegaeon/cache_transfer.py:48-94).
+ *
+ * Cache groups g < num_groups: group_kind[g] (0 = attention, 1 = mamba_none
+ * state page), group_block_size[g] and group_kernel_block_size[g] in tokens,
+ * group_sliding_window[g] (<= 0: no window). Table t < num_tables has
+ * processed_tokens[t] committed tokens; its group-g columns are
+ * column_ids[column_offsets[t*num_groups+g] .. column_offsets[t*num_groups+g+1]),
+ * -1 marking a released column. For every retained column (not released,
+ * not wholly before the group's window) one row is written, in table, group,
+ * column order: out_table, out_group, out_column, out_block (the column's
+ * block id), out_first / out_count (the live kernel-block extent; a state
+ * page is (0, 1)). Any out_* pointer may be null. *num_rows receives the
+ * row count; AEGKV_ENOMEM if it would exceed max_rows.
+ */
+int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
+                           const int64_t* group_block_size,
+                           const int64_t* group_kernel_block_size,
+                           const int64_t* group_sliding_window, int64_t num_tables,
+                           const int64_t* processed_tokens, const int64_t* column_offsets,
+                           const int64_t* column_ids, int64_t max_rows, int64_t* out_table,
+                           int32_t* out_group, int64_t* out_column, int64_t* out_block,
+                           int64_t* out_first, int64_t* out_count, int64_t* num_rows);
+
+/*
  * Pinned host pool. Replaces the pinning half of the reference's host KV
  * pool set-up: Controller._init_cpu_cache (aegaeon/llm.py:1020-1040) and
  * the worker's cudaHostRegister of that mapping (aegaeon/worker.py:251-273).

@@ -656,3 +656,46 @@ def test_swap_waits_on_ipc_event_from_another_process(gpu):
         if child.is_alive():
             child.kill()
     pool.free()
+
+
+def test_tensor_parallel_ranks_share_host_pages(gpu):
+    """Two TP ranks' swappers write disjoint halves of the same host
+    composite pages (host offset tp_rank * composite, worker.py:2304-2309);
+    each rank's bytes survive the other's swap and come back exactly."""
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import allocate_composite_cache, kv_tensor_specs
+    from aegaeon_amd.swapper import KVSwapper
+
+    n_blocks, n_host = 32, 12
+    specs = kv_tensor_specs(3, n_blocks, 16, 2, 64, 2)
+    caches = [allocate_composite_cache(specs, n_blocks, gpu) for _ in range(2)]
+    for c in caches:
+        for t in c.backing:
+            t.random_(-128, 127)
+    composite = caches[0].page_size_bytes
+    pool = ops.PinnedHostPool(n_host * composite * 2)
+    pool.tensor.zero_()
+    names = [{f"layers.{l}.{kv}" for l in range(3) for kv in ("k", "v")}]
+    descr = [CacheGroupRuntimeConfig("attention", 16, 16)]
+    sw = [KVSwapper(c, names, descr, pool.tensor, tp_rank=r, tp_size=2)
+          for r, c in enumerate(caches)]
+    src, host = [3, 9, 17, 30], [0, 5, 6, 11]
+    z = [0] * 4
+    before = [[t.clone() for t in c.backing] for c in caches]
+    evs = [s.swap_blocks([1], src, host, z, z, [1] * 4, [None], False) for s in sw]
+    for e in evs:
+        e.synchronize()
+    view = pool.tensor.view(n_host, 2, composite)
+    for r, c in enumerate(caches):
+        for k, (b, h) in enumerate(zip(src, host)):
+            want = torch.cat([t.view(n_blocks, -1)[b].view(torch.uint8) for t in before[r]])
+            assert torch.equal(view[h, r].to(gpu), want), (r, k)
+    back = [20, 21, 22, 23]
+    evs = [s.swap_blocks([1], host, back, z, z, [1] * 4, [None], True) for s in sw]
+    for e in evs:
+        e.synchronize()
+    for r, c in enumerate(caches):
+        for t, t0 in zip(c.backing, before[r]):
+            tv, t0v = t.view(n_blocks, -1), t0.view(n_blocks, -1)
+            assert torch.equal(tv[back], t0v[src]), r
+    pool.free()

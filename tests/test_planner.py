@@ -140,3 +140,45 @@ def test_zero_count_pages_get_destinations_only():
     assert tables[0].group_blocks[0][0] == LOGICAL_NULL_BLOCK_ID
     assert tables[0].group_blocks[0][1] >= 0
     assert sorted(plan.release_source_block_ids) == [7, 8]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_native_transfer_entries_match_block_table(aegkv_lib, seed):
+    """aegkv_transfer_entries (libaegkv, host-only) equals
+    BlockTable.transfer_entries on random tables with windows, released
+    columns and state pages."""
+    from aegaeon_amd.planner import native_transfer_entries
+
+    rng = random.Random(100 + seed)
+    groups = (CacheGroupConfig("attention", rng.choice([16, 32, 64]), 16),
+              CacheGroupConfig("attention", 48, 16, sliding_window=rng.randint(1, 90)),
+              CacheGroupConfig("mamba_none", 4, 4),
+              CacheGroupConfig("attention", 32, 8, sliding_window=rng.randint(1, 40)))
+    tables = []
+    next_id = 1
+    for _ in range(rng.randint(1, 12)):
+        tokens = rng.randint(0, 400)
+        cols = []
+        for g in groups:
+            n = g.table_blocks_for_tokens(tokens)
+            cols.append(list(range(next_id, next_id + n)))
+            next_id += n
+        t = BlockTable(0, SHAPE, groups, cols)
+        if rng.random() < 0.5:
+            t.release_skipped_blocks(tokens)
+        tables.append((t, tokens))
+    native = native_transfer_entries(groups, tables)
+    for (t, tokens), rows in zip(tables, native):
+        assert rows == t.transfer_entries(tokens)
+
+
+def test_native_transfer_entries_rejections(aegkv_lib):
+    from aegaeon_amd.planner import native_transfer_entries
+
+    t = BlockTable(0, SHAPE, GROUPS, [[5, -7], [], [3]])
+    with pytest.raises(ValueError):
+        native_transfer_entries(GROUPS, [(t, 40)])     # id below the released marker
+    t2 = BlockTable(0, SHAPE, GROUPS, [[5], [6]])
+    with pytest.raises(ValueError):
+        native_transfer_entries(GROUPS, [(t2, 10)])    # column lists per group missing
+    assert native_transfer_entries(GROUPS, []) == []
