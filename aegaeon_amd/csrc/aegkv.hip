@@ -82,6 +82,7 @@ struct Tunables {
   int64_t copy_wgs_per_cu = 0;   // copy_blocks: 0 = one workgroup per work item
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
+  int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
 };
 Tunables g_tune;
 std::mutex g_tune_mu;
@@ -282,11 +283,20 @@ struct Ring {
   std::vector<hipEvent_t> spare;
 };
 
+constexpr int kMaxDmaStreams = 4;
+
 struct DeviceCtx {
   int device = -1;
   int num_cus = 0;
   std::mutex mu;
   Ring ring;
+  // STAGED mode: library-owned streams the per-run copies fan out over,
+  // forked from and joined back into the caller's stream with events.
+  std::mutex dma_mu;
+  int dma_streams = 0;
+  hipStream_t dma[kMaxDmaStreams] = {};
+  hipEvent_t fork_ev = nullptr;
+  hipEvent_t join_ev[kMaxDmaStreams] = {};
 };
 
 std::mutex g_ctx_mu;
@@ -745,6 +755,57 @@ void entry_runs(const SwapLayout& L, const SwapList& E, int64_t i, bool is_swap_
   }
 }
 
+// Create the context's DMA streams and events once (caller holds dma_mu).
+int ensure_dma(DeviceCtx* ctx, int k) {
+  if (!ctx->fork_ev) AEGKV_HIP(hipEventCreateWithFlags(&ctx->fork_ev, hipEventDisableTiming));
+  while (ctx->dma_streams < k) {
+    const int i = ctx->dma_streams;
+    AEGKV_HIP(hipStreamCreateWithFlags(&ctx->dma[i], hipStreamNonBlocking));
+    AEGKV_HIP(hipEventCreateWithFlags(&ctx->join_ev[i], hipEventDisableTiming));
+    ++ctx->dma_streams;
+  }
+  return 0;
+}
+
+// Copy the staged runs between staging and the host pool. With k > 1 the
+// copies fan out over the context's DMA streams, balanced by bytes (fork
+// after everything the caller's stream holds, join before anything it
+// enqueues next), which overlaps the runtime's per-copy gaps.
+int issue_runs(DeviceCtx* ctx, const std::vector<Run>& runs, bool to_device, char* staging,
+               char* host, hipStream_t caller, int k) {
+  const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+  auto copy = [&](const Run& r, hipStream_t st) -> hipError_t {
+    char* s_ptr = staging + r.stage_off;
+    char* h_ptr = host + r.host_off;
+    return to_device ? hipMemcpyAsync(s_ptr, h_ptr, static_cast<size_t>(r.len), kind, st)
+                     : hipMemcpyAsync(h_ptr, s_ptr, static_cast<size_t>(r.len), kind, st);
+  };
+  if (k <= 1) {
+    for (const Run& r : runs) {
+      hipError_t e = copy(r, caller);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staged run)");
+    }
+    return 0;
+  }
+  std::lock_guard<std::mutex> lk(ctx->dma_mu);
+  int rc = ensure_dma(ctx, k);
+  if (rc) return rc;
+  AEGKV_HIP(hipEventRecord(ctx->fork_ev, caller));
+  for (int i = 0; i < k; ++i) AEGKV_HIP(hipStreamWaitEvent(ctx->dma[i], ctx->fork_ev, 0));
+  std::vector<int64_t> load(static_cast<size_t>(k), 0);
+  for (const Run& r : runs) {
+    const int i = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
+    load[static_cast<size_t>(i)] += r.len;
+    hipError_t e = copy(r, ctx->dma[i]);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staged run)");
+  }
+  for (int i = 0; i < k; ++i) {
+    AEGKV_HIP(hipEventRecord(ctx->join_ev[i], ctx->dma[i]));
+    AEGKV_HIP(hipStreamWaitEvent(caller, ctx->join_ev[i], 0));
+  }
+  return 0;
+}
+
 int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
               hipStream_t stream) {
   if (mode < AEGKV_MODE_AUTO || mode > AEGKV_MODE_STAGED)
@@ -792,10 +853,13 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
     void* staging = nullptr;
     AEGKV_HIP(hipMallocAsync(&staging, static_cast<size_t>(m * composite), stream));
     char* st = static_cast<char*>(staging);
+    const int k = static_cast<int>(std::min<int64_t>(t.staged_dma_streams, kMaxDmaStreams));
     if (is_swap_in) {
-      for (const Run& r : runs)
-        AEGKV_HIP(hipMemcpyAsync(st + r.stage_off, L.host_pool + r.host_off,
-                                 static_cast<size_t>(r.len), hipMemcpyHostToDevice, stream));
+      rc = issue_runs(ctx, runs, true, st, L.host_pool, stream, k);
+      if (rc) {
+        (void)hipFreeAsync(staging, stream);
+        return rc;
+      }
     }
     {
       std::lock_guard<std::mutex> lk(ctx->mu);
@@ -807,9 +871,11 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
       return rc;
     }
     if (!is_swap_in) {
-      for (const Run& r : runs)
-        AEGKV_HIP(hipMemcpyAsync(L.host_pool + r.host_off, st + r.stage_off,
-                                 static_cast<size_t>(r.len), hipMemcpyDeviceToHost, stream));
+      rc = issue_runs(ctx, runs, false, st, L.host_pool, stream, k);
+      if (rc) {
+        (void)hipFreeAsync(staging, stream);
+        return rc;
+      }
     }
     AEGKV_HIP(hipFreeAsync(staging, stream));
   }
@@ -839,6 +905,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_COPY_WGS_PER_CU: slot = &g_tune.copy_wgs_per_cu; break;
     case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
     case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
+    case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -855,6 +922,8 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "copy workgroups per CU must be in [0, 64]");
     if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && !valid_copy_unroll(value))
       return fail(AEGKV_EINVAL, "copy unroll must be 0 (auto) or one of 1,2,3,4,5,6,8,10");
+    if (key == AEGKV_TUNE_STAGED_DMA_STREAMS && value > kMaxDmaStreams)
+      return fail(AEGKV_EINVAL, "staged DMA streams must be in [0, %d]", kMaxDmaStreams);
     if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
     *slot = value;

@@ -11,6 +11,7 @@ libaegkv.so; there is no Python or CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Sequence
 
 import numpy as np
@@ -249,12 +250,22 @@ def copy_blocks(
     _lib.check(rc)
 
 
+def _free_pinned(ptr: int) -> None:
+    rc = _lib.load().aegkv_host_free(ptr)
+    if rc:
+        raise _lib.AegkvError(rc, _lib.load().aegkv_last_error().decode(errors="replace"))
+
+
 class PinnedHostPool:
     """A pinned, device-mapped host byte pool from aegkv_host_alloc.
 
     Counterpart of the reference's host KV pool (aegaeon/llm.py:1020-1040,
     aegaeon/worker.py:251-273), allocated pinned instead of registering an
     existing /dev/shm mapping. `tensor` is a uint8 view of the whole pool.
+    The memory is released when the pool and every tensor viewing it are
+    gone (views keep it alive), so a kernel can never be handed freed
+    memory through a surviving view. Callers still wait for GPU work on the
+    pool before dropping the last view.
     """
 
     def __init__(self, nbytes: int):
@@ -263,19 +274,12 @@ class PinnedHostPool:
         lib = _lib.load()
         ptr = ctypes.c_void_p()
         _lib.check(lib.aegkv_host_alloc(ctypes.byref(ptr), int(nbytes)))
-        self._ptr = ptr.value
         self.nbytes = int(nbytes)
-        buf = (ctypes.c_uint8 * self.nbytes).from_address(self._ptr)
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(ptr.value)
+        fin = weakref.finalize(buf, _free_pinned, ptr.value)
+        fin.atexit = False  # at interpreter exit the process releases it
         self.tensor = torch.frombuffer(buf, dtype=torch.uint8)
 
     def free(self) -> None:
-        if self._ptr:
-            self.tensor = None
-            _lib.check(_lib.load().aegkv_host_free(self._ptr))
-            self._ptr = None
-
-    def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
+        """Drop this pool's reference; the memory goes once no view remains."""
+        self.tensor = None

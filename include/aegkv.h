@@ -63,6 +63,9 @@ extern "C" {
 #define AEGKV_TUNE_SWAP_SHAPE_AUTO 8 /* 1: swap kernels pick their shape
                                         from the page size like copy_blocks */
 #define AEGKV_TUNE_SWAP_IN_WORKGROUPS 9 /* swap-in kernel: workgroups      */
+#define AEGKV_TUNE_STAGED_DMA_STREAMS 10 /* STAGED copies fan out over this
+                                          many library streams (0-4; <= 1:
+                                          all on the caller's stream)     */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

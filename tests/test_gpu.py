@@ -183,7 +183,8 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
 @pytest.fixture
 def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
-            _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES)
+            _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
+            _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -253,6 +254,48 @@ def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, w
         for s in range(len(page)):
             assert np.array_equal(segs[s].cpu().numpy(), want_segs[s]), (mode, s)
         pool.free()
+
+
+@pytest.mark.parametrize("dma_streams", [0, 1, 3, 4])
+def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
+    """STAGED copies forked over 0-4 library streams (and split into small
+    staging chunks) land exactly where the oracle puts them, both ways."""
+    _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, dma_streams)
+    _lib.tune(_lib.TUNE_STAGING_BYTES, 1 << 20)
+    rng = np.random.default_rng(50 + dma_streams)
+    page = np.array([64 * 1024, 16 * 1024, 48 * 1024], np.int64)
+    cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)
+    owners = np.ones(3, np.uint64)
+    kpp = np.array([4], np.int64)
+    composite = int(page.sum())
+    n_gpu, n_host, n = 40, 48, 33
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    src = rng.permutation(n_gpu)[:n]
+    dst = np.sort(rng.permutation(n_host)[:n])  # partly contiguous host runs
+    first = rng.integers(0, 2, n)
+    valid = np.array([rng.integers(0, 4 - f + 1) for f in first])
+    grp = np.zeros(n, np.int32)
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    pool = ops.PinnedHostPool(n_host * composite)
+    pool.tensor.zero_()
+    common = (page, cpu_off, owners, n_gpu, kpp, pool.tensor, composite, 0)
+    ops.swap_segments(segs, *common, src, dst, grp, first, valid, False, mode="staged")
+    want = np.zeros((n_host, composite), np.uint8)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       want.reshape(-1), composite, 0, composite, src, dst, grp, first, valid,
+                       False)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.tensor.numpy().reshape(want.shape), want)
+    back = rng.permutation(n_gpu)[:n]
+    ops.swap_segments(segs, *common, dst, back, grp, first, valid, True, mode="staged")
+    want_segs = [x.copy() for x in segs_np]
+    oracle.swap_blocks([x.reshape(-1) for x in want_segs], page, cpu_off, owners, n_gpu, kpp,
+                       want.reshape(-1), composite, 0, composite, dst, back, grp, first, valid,
+                       True)
+    torch.cuda.synchronize()
+    for s in range(3):
+        assert np.array_equal(segs[s].cpu().numpy(), want_segs[s]), s
+    pool.free()
 
 
 # --------------------------------------------------------- error behaviour --
