@@ -51,6 +51,9 @@ def parse():
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--no-reference-loop", action="store_true",
+                   help="skip timing the reference per-extent copy loop on the GPU "
+                        "(about 147k copy_ calls; very slow under a memory-copy trace)")
     p.add_argument("--config", default="headline",
                    choices=["headline", "varlen", "overlap", "refplan"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
@@ -720,28 +723,30 @@ def main():
     }
     # The reference's own data path on this GPU: Worker.swap_blocks' loop of
     # one copy_(non_blocking=True) per (segment, block) tile, same blocks.
-    log("timing the reference per-extent copy loop on the same GPU")
-    pages1 = [t.view(torch.uint8).view(NB1, tile1) for t in segs1]
-    hv = pool.tensor.view(HOST1, S1 * tile1)
-    ref = {}
-    for name, src_l, dst_l, is_in in (("d2h", out_ids.tolist(), host_ids.tolist(), False),
-                                      ("h2d", host_ids.tolist(), in_ids.tolist(), True)):
-        reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)  # warm-up
-        a, b = ev_pair(torch)
-        a.record()
-        reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)
-        b.record()
-        b.synchronize()
-        ref[name] = swap_bytes / (a.elapsed_time(b) / 1e3) / 1e9
-    if not all(torch.equal(s[di], s[do]) for s in segs1):
-        raise AssertionError("reference-loop round trip is not bit-exact")
-    line["reference_path_same_gpu"] = {
-        "what": "reference per-extent copy_ loop (aegaeon/worker.py:2272-2328), 73,728 "
-                "copies per direction, same blocks and pool",
-        "d2h_GBps": round(ref["d2h"], 3), "h2d_GBps": round(ref["h2d"], 3),
-        "speedup_d2h": round(d2h_gbps / ref["d2h"], 2),
-        "speedup_h2d": round(h2d_gbps / ref["h2d"], 2),
-    }
+    line["reference_path_same_gpu"] = None
+    if not args.no_reference_loop:
+        pages1 = [t.view(torch.uint8).view(NB1, tile1) for t in segs1]
+        hv = pool.tensor.view(HOST1, S1 * tile1)
+        ref = {}
+        for name, src_l, dst_l, is_in in (("d2h", out_ids.tolist(), host_ids.tolist(), False),
+                                          ("h2d", host_ids.tolist(), in_ids.tolist(), True)):
+            log(f"timing the reference per-extent copy loop on the same GPU ({name})")
+            reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)  # warm-up
+            a, b = ev_pair(torch)
+            a.record()
+            reference_worker_loop(pages1, hv, tile1, src_l, dst_l, is_in)
+            b.record()
+            b.synchronize()
+            ref[name] = swap_bytes / (a.elapsed_time(b) / 1e3) / 1e9
+        if not all(torch.equal(s[di], s[do]) for s in segs1):
+            raise AssertionError("reference-loop round trip is not bit-exact")
+        line["reference_path_same_gpu"] = {
+            "what": "reference per-extent copy_ loop (aegaeon/worker.py:2272-2328), 73,728 "
+                    "copies per direction, same blocks and pool",
+            "d2h_GBps": round(ref["d2h"], 3), "h2d_GBps": round(ref["h2d"], 3),
+            "speedup_d2h": round(d2h_gbps / ref["d2h"], 2),
+            "speedup_h2d": round(h2d_gbps / ref["h2d"], 2),
+        }
     pool.free()
     del segs1, segs2
     torch.cuda.empty_cache()
