@@ -1,8 +1,8 @@
 /*
  * aegkv_oracle.c - CPU restatement of the reference's KV movement path.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker the tests, the smoke
- * run and the benchmark's CPU-baseline leg compare libaegkv against. The
+ * TEST INFRASTRUCTURE ONLY. This file is the reference restatement the tests,
+ * the smoke run and the benchmark's CPU-baseline leg compare libaegkv against. The
  * product (aegaeon_amd/, libaegkv.so) never links, loads or calls it.
  *
  * Every function restates one piece of pkusys/Aegaeon, cited by file:line,

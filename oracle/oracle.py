@@ -1,7 +1,7 @@
 """Oracle for the KV movement path: TEST INFRASTRUCTURE, never product code.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, and only as the checker / CPU baseline. It wraps the plain-C
+this module, and only to check results / time the CPU baseline. It wraps the plain-C
 restatement in aegkv_oracle.c (built by oracle/build.py into
 oracle/liboracle_aegkv.so) and adds `swap_blocks_torch`, a torch-on-host
 restatement of the reference's per-extent copy_ loop that the CPU baseline

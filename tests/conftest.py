@@ -35,8 +35,7 @@ def golden():
 
 @pytest.fixture(scope="session")
 def aegkv_lib():
-    """The built C-ABI library (built here if the tree has none yet; the GPU
-    box always receives a prebuilt one)."""
+    """The built C-ABI library (compiled here if the tree has none yet)."""
     from aegaeon_amd import _lib, build
 
     if not _lib.LIB_PATH.exists():

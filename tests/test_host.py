@@ -250,3 +250,14 @@ def test_tuning_knobs(aegkv_lib):
         _lib.tune(_lib.TUNE_AUTO_D2H, 7)
     with pytest.raises(ValueError):
         _lib.tune(99, 1)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; asking for more exits with a message."""
+    import sys
+
+    res = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr
+    assert res.stdout == ""
