@@ -559,10 +559,14 @@ struct SwapList {
   const int64_t* valid;     // may be null: all kpp[group]
 };
 
-// dev_vec: every device tile extent is 16 B aligned; host_vec: so is every
-// host-pool extent. The 16 B kernel path needs both sides aligned.
-int validate_layout(const SwapLayout& L, bool direct, int64_t* composite_bytes,
-                    bool* dev_vec, bool* host_vec) {
+bool mul_fits(int64_t a, int64_t b) { return a >= 0 && b >= 0 && (b == 0 || a <= INT64_MAX / b); }
+
+// Argument checks that need no HIP call (run first, so a bad argument costs
+// nothing on the device side). dev_vec: every device tile extent is 16 B
+// aligned; host_vec: so is every host-pool extent. The 16 B kernel path needs
+// both sides aligned.
+int validate_layout(const SwapLayout& L, int64_t* composite_bytes, bool* dev_vec,
+                    bool* host_vec) {
   if (L.num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
   if (!L.bases || !L.page_bytes || !L.host_offsets || !L.owner_masks)
     return fail(AEGKV_EINVAL, "segment arrays must not be null");
@@ -573,10 +577,15 @@ int validate_layout(const SwapLayout& L, bool direct, int64_t* composite_bytes,
   if (!L.host_pool) return fail(AEGKV_EINVAL, "host_pool must not be null");
   if (L.host_num_blocks <= 0 || L.host_page_bytes <= 0)
     return fail(AEGKV_EINVAL, "host pool geometry must be positive");
-  if (L.host_rank_offset < 0) return fail(AEGKV_EINVAL, "host_rank_offset must be >= 0");
+  if (!mul_fits(L.host_num_blocks, L.host_page_bytes))
+    return fail(AEGKV_ERANGE, "host pool of %lld x %lld bytes overflows",
+                static_cast<long long>(L.host_num_blocks),
+                static_cast<long long>(L.host_page_bytes));
+  if (L.host_rank_offset < 0 || L.host_rank_offset >= L.host_page_bytes)
+    return fail(AEGKV_EINVAL, "host_rank_offset must be in [0, host_page_bytes)");
   for (int32_t g = 0; g < L.num_groups; ++g)
-    if (L.kpp[g] <= 0)
-      return fail(AEGKV_EINVAL, "kernel_blocks_per_page[%d]=%lld must be positive", g,
+    if (L.kpp[g] <= 0 || L.kpp[g] > INT32_MAX)
+      return fail(AEGKV_EINVAL, "kernel_blocks_per_page[%d]=%lld must be in [1, 2^31)", g,
                   static_cast<long long>(L.kpp[g]));
   bool v = true;
   int64_t composite = 0;
@@ -586,7 +595,12 @@ int validate_layout(const SwapLayout& L, bool direct, int64_t* composite_bytes,
     if (!L.bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
     if (pb <= 0) return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
     if (ho < 0) return fail(AEGKV_EINVAL, "segment %d host offset must be >= 0", s);
-    if (L.host_rank_offset + ho + pb > L.host_page_bytes)
+    if (!mul_fits(L.device_num_blocks, pb))
+      return fail(AEGKV_ERANGE, "segment %d of %lld x %lld bytes overflows", s,
+                  static_cast<long long>(L.device_num_blocks), static_cast<long long>(pb));
+    // rank offset + host offset + page must stay inside one host page
+    if (ho > L.host_page_bytes || pb > L.host_page_bytes - ho ||
+        L.host_rank_offset > L.host_page_bytes - ho - pb)
       return fail(AEGKV_ERANGE,
                   "segment %d [%lld, +%lld) at rank offset %lld overruns the %lld-byte host page",
                   s, static_cast<long long>(ho), static_cast<long long>(pb),
@@ -600,21 +614,30 @@ int validate_layout(const SwapLayout& L, bool direct, int64_t* composite_bytes,
                     static_cast<long long>(pb), static_cast<long long>(L.kpp[g]));
     if (L.num_groups < 64 && (L.owner_masks[s] >> L.num_groups) != 0)
       return fail(AEGKV_ERANGE, "segment %d owner mask names a group >= %d", s, L.num_groups);
-    int rc = check_device_range(L.bases[s], L.device_num_blocks * pb, "segment base");
-    if (rc) return rc;
     v = v && aligned16(L.bases[s]) && pb % 16 == 0 && ho % 16 == 0;
     for (int32_t g = 0; g < L.num_groups && v; ++g)
       if ((L.owner_masks[s] >> g) & 1ull) v = (pb / L.kpp[g]) % 16 == 0;
     composite = std::max(composite, ho + pb);
   }
-  if (direct) {
-    int rc = check_host_range(L.host_pool, L.host_num_blocks * L.host_page_bytes, "host_pool");
-    if (rc) return rc;
-  }
   *composite_bytes = composite;
   *dev_vec = v;
   *host_vec = aligned16(L.host_pool) && L.host_page_bytes % 16 == 0 &&
               L.host_rank_offset % 16 == 0;
+  return 0;
+}
+
+// Pointer checks through the HIP runtime: every segment lies inside one
+// device allocation; in DIRECT mode the host pool is pinned and mapped.
+int check_layout_pointers(const SwapLayout& L, bool direct) {
+  for (int32_t s = 0; s < L.num_segments; ++s) {
+    int rc = check_device_range(L.bases[s], L.device_num_blocks * L.page_bytes[s],
+                                "segment base");
+    if (rc) return rc;
+  }
+  if (direct) {
+    int rc = check_host_range(L.host_pool, L.host_num_blocks * L.host_page_bytes, "host_pool");
+    if (rc) return rc;
+  }
   return 0;
 }
 
@@ -645,7 +668,7 @@ int validate_list(const SwapLayout& L, const SwapList& E, bool is_swap_in) {
     const int64_t k = L.kpp[g];
     const int64_t first = E.first ? E.first[i] : 0;
     const int64_t valid = E.valid ? E.valid[i] : k;
-    if (first < 0 || valid < 0 || first + valid > k)
+    if (first < 0 || valid < 0 || first > k || valid > k - first)
       return fail(AEGKV_EEXTENT, "kernel-block extent [%lld, %lld) at %lld exceeds page size %lld",
                   static_cast<long long>(first), static_cast<long long>(first + valid),
                   static_cast<long long>(i), static_cast<long long>(k));
@@ -816,11 +839,13 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   const bool staged = mode == AEGKV_MODE_STAGED;
   int64_t composite = 0;
   bool dev_vec = false, host_vec = false;
-  int rc = validate_layout(L, !staged, &composite, &dev_vec, &host_vec);
+  int rc = validate_layout(L, &composite, &dev_vec, &host_vec);
   if (rc) return rc;
   rc = validate_list(L, E, is_swap_in);
   if (rc) return rc;
   if (E.n == 0) return 0;
+  rc = check_layout_pointers(L, !staged);
+  if (rc) return rc;
   DeviceCtx* ctx = nullptr;
   rc = get_ctx(&ctx);
   if (rc) return rc;
@@ -988,9 +1013,10 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
     if (!segment_bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
     if (segment_page_bytes[s] <= 0)
       return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
-    int rc = check_device_range(segment_bases[s], device_num_blocks * segment_page_bytes[s],
-                                "segment base");
-    if (rc) return rc;
+    if (!mul_fits(device_num_blocks, segment_page_bytes[s]))
+      return fail(AEGKV_ERANGE, "segment %d of %lld x %lld bytes overflows", s,
+                  static_cast<long long>(device_num_blocks),
+                  static_cast<long long>(segment_page_bytes[s]));
     vec = vec && aligned16(segment_bases[s]) && segment_page_bytes[s] % 16 == 0;
     max_page = std::max(max_page, segment_page_bytes[s]);
   }
@@ -1017,6 +1043,11 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
     role[static_cast<size_t>(s)] = 1;
   }
   if (num_pairs == 0) return 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    int rc = check_device_range(segment_bases[s], device_num_blocks * segment_page_bytes[s],
+                                "segment base");
+    if (rc) return rc;
+  }
   const Tunables t = tunables();
   ShapeSel sh = auto_shape(max_page);
   if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};

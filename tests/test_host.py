@@ -261,3 +261,64 @@ def test_bench_refuses_more_than_one_gpu():
     assert res.returncode == 2
     assert "one GPU" in res.stderr
     assert res.stdout == ""
+
+
+def _swap_blocks_call(lib, *, n_seg=2, page=(4096, 4096), hoff=(0, 4096), owners=(1, 1),
+                      dev_blocks=8, kpp=(4,), host_blocks=6, host_page=8192, rank_off=0,
+                      src=(1,), dst=(2,), grp=(0,), first=(0,), valid=(4,), is_in=0, mode=1):
+    """Call aegkv_swap_blocks with placeholder (never dereferenced) pointers:
+    every case here must be rejected before any HIP call."""
+    import numpy as np
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+    arr = lambda x, t=np.int64: np.ascontiguousarray(np.array(x, dtype=t))  # noqa: E731
+    keep = [arr(page), arr(hoff), arr(owners, np.uint64), arr(kpp), arr(src), arr(dst),
+            arr(grp, np.int32), arr(first), arr(valid)]
+    bases = (ctypes.c_void_p * n_seg)(*[0x10000 + 0x100000 * i for i in range(n_seg)])
+    p = lambda a, t=P64: a.ctypes.data_as(t)  # noqa: E731
+    return lib.aegkv_swap_blocks(
+        n_seg, bases, p(keep[0]), p(keep[1]), p(keep[2], ctypes.POINTER(ctypes.c_uint64)),
+        dev_blocks, len(kpp), p(keep[3]), ctypes.c_void_p(0x7000000), host_blocks, host_page,
+        rank_off, len(src), p(keep[4]), p(keep[5]), p(keep[6], ctypes.POINTER(ctypes.c_int32)),
+        p(keep[7]), p(keep[8]), is_in, mode, None)
+
+
+@pytest.mark.parametrize("kwargs,code,word", [
+    (dict(src=(8,)), -2, "source block id"),
+    (dict(dst=(6,)), -2, "target block id"),
+    (dict(src=(1, 2), dst=(3, 3), grp=(0, 0), first=(0, 0), valid=(4, 4)), -3, "twice"),
+    (dict(grp=(1,)), -2, "group id"),
+    (dict(first=(1,), valid=(4,)), -4, "exceeds page size"),
+    (dict(first=(-1,), valid=(1,)), -4, "exceeds page size"),
+    (dict(kpp=(3,)), -4, "not divisible"),
+    (dict(hoff=(0, 4097)), -2, "overruns"),
+    (dict(rank_off=8192), -1, "host_rank_offset"),
+    (dict(dev_blocks=1 << 62), -2, "overflows"),
+    (dict(host_blocks=1 << 62), -2, "overflows"),
+    (dict(owners=(1, 2)), -2, "owner mask"),
+    (dict(owners=(1, 0)), -1, "no owning group"),
+    (dict(mode=7), -1, "transfer mode"),
+])
+def test_swap_blocks_rejections_before_any_hip_call(aegkv_lib, kwargs, code, word):
+    rc = _swap_blocks_call(aegkv_lib, **kwargs)
+    assert rc == code
+    assert word.encode() in aegkv_lib.aegkv_last_error()
+
+
+def test_copy_blocks_rejections_before_any_hip_call(aegkv_lib):
+    import numpy as np
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+    bases = (ctypes.c_void_p * 1)(0x10000)
+    page = np.array([4096], np.int64)
+
+    def call(src, dst, blocks=8):
+        s, d = np.array(src, np.int64), np.array(dst, np.int64)
+        return aegkv_lib.aegkv_copy_blocks(1, bases, page.ctypes.data_as(P64), blocks, s.size,
+                                           s.ctypes.data_as(P64), d.ctypes.data_as(P64), None)
+
+    assert call([1, 2], [2, 3]) == -5
+    assert call([1, 2], [3, 3]) == -3
+    assert call([1], [8]) == -2
+    assert call([1], [2], blocks=1 << 62) == -2
+    assert call([], []) == 0  # nothing to do, nothing touched
