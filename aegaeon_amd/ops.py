@@ -130,6 +130,104 @@ def swap(
     _lib.check(rc)
 
 
+class _OnDevice:
+    """Make `device` current for a call, switching only when it is not."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, device: torch.device):
+        self.index = device.index if device.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+            self.prev = None
+
+
+class SegmentLayout:
+    """A validated composite layout, reusable across swap calls.
+
+    Holds the backing tensors (segments, each viewed as [device_num_blocks,
+    page] bytes), their composite-page geometry (vllm_cache.py:75-101,
+    worker.py:1419-1432) and the pinned host pool, checked once and kept as
+    the C-ABI arrays the library takes, so a call only converts its id lists.
+    The layout keeps references to the tensors it describes.
+    """
+
+    def __init__(self, segments: Sequence[torch.Tensor], segment_page_bytes: Sequence[int],
+                 segment_host_offsets: Sequence[int], segment_owner_masks: Sequence[int],
+                 device_num_blocks: int, group_kernel_blocks_per_page: Sequence[int],
+                 host_pool: torch.Tensor, host_page_bytes: int, host_rank_offset: int):
+        if not segments:
+            raise ValueError("at least one segment is required")
+        dev = segments[0].device
+        for i, t in enumerate(segments):
+            _require_device(t, f"segment {i}")
+            if t.device != dev:
+                raise ValueError("all segments must live on one device")
+        _require_host(host_pool, "host_pool")
+        n_seg = len(segments)
+        self.page = _i64(segment_page_bytes)
+        self.host_offsets = _i64(segment_host_offsets)
+        self.owners = np.ascontiguousarray(
+            np.asarray(segment_owner_masks, dtype=np.uint64).reshape(-1))
+        self.kpp = _i64(group_kernel_blocks_per_page)
+        if not (self.page.size == self.host_offsets.size == self.owners.size == n_seg):
+            raise ValueError("segment metadata lengths must equal the number of segments")
+        for i, t in enumerate(segments):
+            if _tensor_bytes(t) < int(self.page[i]) * device_num_blocks:
+                raise ValueError(
+                    f"segment {i} holds {_tensor_bytes(t)} bytes < "
+                    f"{device_num_blocks} x {int(self.page[i])}"
+                )
+        self.segments = list(segments)
+        self.host_pool = host_pool
+        self.device = dev
+        self.num_segments = n_seg
+        self.device_num_blocks = int(device_num_blocks)
+        self.host_page_bytes = int(host_page_bytes)
+        self.host_rank_offset = int(host_rank_offset)
+        self.host_num_blocks = (_tensor_bytes(host_pool) // self.host_page_bytes
+                                if self.host_page_bytes > 0 else 0)
+        self._bases = (ctypes.c_void_p * n_seg)(*[t.data_ptr() for t in segments])
+        self._args = (n_seg, self._bases, _p64(self.page), _p64(self.host_offsets),
+                      _pu64(self.owners), self.device_num_blocks, self.kpp.size,
+                      _p64(self.kpp), host_pool.data_ptr(), self.host_num_blocks,
+                      self.host_page_bytes, self.host_rank_offset)
+        self._on_device = _OnDevice(dev)
+
+    def swap(self, source_block_ids, target_block_ids, group_ids, first_kernel_blocks,
+             valid_kernel_blocks, is_swap_in: bool, *, mode="auto",
+             stream: torch.cuda.Stream | None = None) -> None:
+        """One aegkv_swap_blocks call over this layout (see swap_segments)."""
+        src = _i64(source_block_ids)
+        dst = _i64(target_block_ids)
+        grp = _i32(group_ids)
+        first = _i64(first_kernel_blocks)
+        valid = _i64(valid_kernel_blocks)
+        if not (src.size == dst.size == grp.size == first.size == valid.size):
+            raise ValueError(
+                "Swap block ids and metadata must have equal lengths: "
+                f"source={src.size}, target={dst.size}, groups={grp.size}, "
+                f"first={first.size}, valid={valid.size}"
+            )
+        lib = _lib.load()
+        with self._on_device:
+            rc = lib.aegkv_swap_blocks(
+                *self._args, src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
+                _p64(valid), 1 if is_swap_in else 0, _mode(mode),
+                _stream_ptr(self.device, stream),
+            )
+        _lib.check(rc)
+
+
 def swap_segments(
     segments: Sequence[torch.Tensor],
     segment_page_bytes: Sequence[int],
@@ -157,50 +255,14 @@ def swap_segments(
     of (page_s, kernel blocks per page, first, valid) (cache_transfer.py:
     138-165); host bytes sit at host_id * host_page_bytes + host_rank_offset
     + host_offset_s + off; device bytes at dev_id * page_s + off of segment s.
+    Callers that swap over the same layout repeatedly should build a
+    SegmentLayout once and call its swap().
     """
-    if not segments:
-        raise ValueError("at least one segment is required")
-    dev = segments[0].device
-    for i, t in enumerate(segments):
-        _require_device(t, f"segment {i}")
-        if t.device != dev:
-            raise ValueError("all segments must live on one device")
-    _require_host(host_pool, "host_pool")
-    n_seg = len(segments)
-    page = _i64(segment_page_bytes)
-    hoff = _i64(segment_host_offsets)
-    owners = np.ascontiguousarray(np.asarray(segment_owner_masks, dtype=np.uint64).reshape(-1))
-    kpp = _i64(group_kernel_blocks_per_page)
-    if not (page.size == hoff.size == owners.size == n_seg):
-        raise ValueError("segment metadata lengths must equal the number of segments")
-    for i, t in enumerate(segments):
-        if _tensor_bytes(t) < int(page[i]) * device_num_blocks:
-            raise ValueError(
-                f"segment {i} holds {_tensor_bytes(t)} bytes < {device_num_blocks} x {int(page[i])}"
-            )
-    src = _i64(source_block_ids)
-    dst = _i64(target_block_ids)
-    grp = _i32(group_ids)
-    first = _i64(first_kernel_blocks)
-    valid = _i64(valid_kernel_blocks)
-    lengths = {src.size, dst.size, grp.size, first.size, valid.size}
-    if len(lengths) != 1:
-        raise ValueError(
-            "Swap block ids and metadata must have equal lengths: "
-            f"source={src.size}, target={dst.size}, groups={grp.size}, "
-            f"first={first.size}, valid={valid.size}"
-        )
-    bases = (ctypes.c_void_p * n_seg)(*[t.data_ptr() for t in segments])
-    host_blocks = _tensor_bytes(host_pool) // host_page_bytes if host_page_bytes > 0 else 0
-    lib = _lib.load()
-    with torch.cuda.device(dev):
-        rc = lib.aegkv_swap_blocks(
-            n_seg, bases, _p64(page), _p64(hoff), _pu64(owners), int(device_num_blocks),
-            kpp.size, _p64(kpp), host_pool.data_ptr(), host_blocks, int(host_page_bytes),
-            int(host_rank_offset), src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
-            _p64(valid), 1 if is_swap_in else 0, _mode(mode), _stream_ptr(dev, stream),
-        )
-    _lib.check(rc)
+    SegmentLayout(segments, segment_page_bytes, segment_host_offsets, segment_owner_masks,
+                  device_num_blocks, group_kernel_blocks_per_page, host_pool, host_page_bytes,
+                  host_rank_offset).swap(source_block_ids, target_block_ids, group_ids,
+                                         first_kernel_blocks, valid_kernel_blocks, is_swap_in,
+                                         mode=mode, stream=stream)
 
 
 def copy_blocks(

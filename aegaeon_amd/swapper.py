@@ -92,6 +92,10 @@ class KVSwapper:
                 self._extents_per_entry[g] += 1
         device = self._segments[0].device
         self.device = device
+        self._layout = ops.SegmentLayout(
+            self._segments, self._page, self._cpu_off, self._owner_mask, cache.num_blocks,
+            self._kpp, self.kv_swap_view.view(-1), self.host_page_bytes,
+            self.tp_rank * cache.page_size_bytes)
         self.swap_in_stream = torch.cuda.Stream(device)
         self.swap_out_stream = torch.cuda.Stream(device)
         self.move_event_table: Dict[int, List[torch.cuda.Event]] = defaultdict(list)
@@ -134,13 +138,9 @@ class KVSwapper:
                     ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
                 stream.wait_event(ev)
             self.move_event_table[rid].append(new_event)
-        ops.swap_segments(
-            self._segments, self._page, self._cpu_off, self._owner_mask,
-            self.cache.num_blocks, self._kpp, self.kv_swap_view.view(-1),
-            self.host_page_bytes, self.tp_rank * self.cache.page_size_bytes,
-            source_block_ids, target_block_ids, groups.astype(np.int32),
-            first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode, stream=stream,
-        )
+        self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
+                          first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
+                          stream=stream)
         new_event.record(stream)
         if logger.isEnabledFor(logging.INFO):
             valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)

@@ -245,22 +245,23 @@ def bench_varlen(args):
     host_ids = np.array(pools.allocate(total, BLOCK_LOCATION_CPU, (page // 2,)), np.int64)
     pool = ops.PinnedHostPool(n_slabs * slab)
     common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    lay = ops.SegmentLayout(segs, *common)
     z = np.zeros(total, np.int32)
     one = np.ones(total, np.int64)
     res = {}
     for mode in ("direct", "staged"):
         for _ in range(args.warmup):
-            ops.swap_segments(segs, *common, out_ids, host_ids, z, z, one, False, mode=mode)
-            ops.swap_segments(segs, *common, host_ids, in_ids, z, z, one, True, mode=mode)
+            lay.swap(out_ids, host_ids, z, z, one, False, mode=mode)
+            lay.swap(host_ids, in_ids, z, z, one, True, mode=mode)
         outs, ins = [], []
         for _ in range(args.steps):
             a, b = ev_pair(torch)
             c, d = ev_pair(torch)
             a.record()
-            ops.swap_segments(segs, *common, out_ids, host_ids, z, z, one, False, mode=mode)
+            lay.swap(out_ids, host_ids, z, z, one, False, mode=mode)
             b.record()
             c.record()
-            ops.swap_segments(segs, *common, host_ids, in_ids, z, z, one, True, mode=mode)
+            lay.swap(host_ids, in_ids, z, z, one, True, mode=mode)
             d.record()
             outs.append((a, b))
             ins.append((c, d))
@@ -326,11 +327,12 @@ def bench_overlap(args):
     host_out = rng.permutation(NOUT + NIN)
     host_x, host_y = host_out[:NOUT], host_out[NOUT:]
     common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    lay = ops.SegmentLayout(segs, *common)
     zo, oo = np.zeros(NOUT, np.int32), np.ones(NOUT, np.int64)
     zi, oi = np.zeros(NIN, np.int32), np.ones(NIN, np.int64)
     # the incoming model's blocks were swapped out earlier: put them on the
     # host, remember their checksums, and clear them on the device
-    ops.swap_segments(segs, *common, in_ids, host_y, zi, zi, oi, False)
+    lay.swap(in_ids, host_y, zi, zi, oi, False)
     di = torch.from_numpy(in_ids).to(dev)
     want_in = [t[di].view(NIN, -1).view(torch.int16).sum(dim=1, dtype=torch.int64) for t in segs]
     for t in segs:
@@ -350,11 +352,11 @@ def bench_overlap(args):
             st.wait_event(begin)
         with torch.cuda.stream(streams[0]):
             evs[0][0].record()
-            ops.swap_segments(segs, *common, out_ids, host_x, zo, zo, oo, False)
+            lay.swap(out_ids, host_x, zo, zo, oo, False)
             evs[0][1].record()
         with torch.cuda.stream(streams[1]):
             evs[1][0].record()
-            ops.swap_segments(segs, *common, host_y, in_ids, zi, zi, oi, True)
+            lay.swap(host_y, in_ids, zi, zi, oi, True)
             evs[1][1].record()
         with torch.cuda.stream(streams[2]):
             evs[2][0].record()
@@ -482,6 +484,9 @@ def bench_refplan(args):
             t.random_(0, 256)
         ids = np.arange(pages)
         host_view = host.tensor.view(pages, phys_bytes)
+        plan_lay = ops.SegmentLayout(segs, [seg_page] * seg_n,
+                                     [s * seg_page for s in range(seg_n)], [1] * seg_n, pages,
+                                     [kpp], host.tensor, phys_bytes, 0)
         row = {"length": length, "pages": pages}
         for name, plan in plans.items():
             first = np.array([f for f, _ in plan], np.int64)
@@ -490,10 +495,7 @@ def bench_refplan(args):
             moved = int(valid.sum()) * (seg_page // kpp) * seg_n
             row[f"{name}_bytes"] = moved
             for direction, is_in in (("H2D", True), ("D2H", False)):
-                t_aeg = p50(lambda: ops.swap_segments(
-                    segs, [seg_page] * seg_n, [s * seg_page for s in range(seg_n)],
-                    [1] * seg_n, pages, [kpp], host.tensor, phys_bytes, 0, ids, ids, grp,
-                    first, valid, is_in))
+                t_aeg = p50(lambda: plan_lay.swap(ids, ids, grp, first, valid, is_in))
                 extents = [byte_extent_for_kernel_blocks(seg_page, kpp, f, c) for f, c in plan]
                 t_ref = p50(lambda: reference_submit_copies(host_view, segs, extents, is_in))
                 row[f"{name}_{direction}_ms"] = {"aegkv": round(t_aeg, 4),
@@ -508,7 +510,7 @@ def bench_refplan(args):
                         host_view[pg, s * seg_page + lo:s * seg_page + hi]):
                     raise AssertionError(f"refplan mismatch at length {length}")
         out.append(row)
-        del segs
+        del segs, plan_lay
         host.free()
 
     # Qwen3-4B: 1024 scattered blocks each way, whole tiles.
@@ -524,9 +526,10 @@ def bench_refplan(args):
     in_ids = rest[torch.randperm(rest.size, generator=g)[:n].numpy()]
     common = ([tile1] * S1, [i * tile1 for i in range(S1)], [1] * S1, NB1, [1], pool.tensor,
               S1 * tile1, 0)
+    lay = ops.SegmentLayout(segs1, *common)
     z, one = np.zeros(n, np.int32), np.ones(n, np.int64)
-    t_out = p50(lambda: ops.swap_segments(segs1, *common, out_ids, host_ids, z, z, one, False))
-    t_in = p50(lambda: ops.swap_segments(segs1, *common, host_ids, in_ids, z, z, one, True))
+    t_out = p50(lambda: lay.swap(out_ids, host_ids, z, z, one, False))
+    t_in = p50(lambda: lay.swap(host_ids, in_ids, z, z, one, True))
     pl_out, pl_h, pl_in = out_ids.tolist(), host_ids.tolist(), in_ids.tolist()
     r_out = p50(lambda: reference_worker_loop(pages1, hv, tile1, pl_out, pl_h, False))
     r_in = p50(lambda: reference_worker_loop(pages1, hv, tile1, pl_h, pl_in, True))
@@ -534,8 +537,34 @@ def bench_refplan(args):
     di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
     if not all(torch.equal(t[di], t[do]) for t in segs1):
         raise AssertionError("Qwen3-4B reference-loop round trip not bit-exact")
+    # wall-clock latency of one swap-out call (host work + transfer), small to
+    # large, as a model switch sees it
+    latency = []
+    for nb in (1, 4, 16, 64, 256, 1024):
+        o_ids, h_ids = out_ids[:nb], host_ids[:nb]
+        zz, oo = np.zeros(nb, np.int32), np.ones(nb, np.int64)
+        pl_o, pl_h = o_ids.tolist(), h_ids.tolist()
+
+        def wall(fn, reps=max(3, min(20, 2048 // nb))):
+            fn()
+            torch.cuda.synchronize()
+            samples = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                samples.append((time.perf_counter() - t0) * 1e3)
+            return statistics.median(samples)
+
+        latency.append({
+            "blocks": nb, "bytes": nb * S1 * tile1,
+            "aegkv_ms": round(wall(lambda: lay.swap(o_ids, h_ids, zz, zz, oo, False)), 4),
+            "reference_loop_ms": round(wall(lambda: reference_worker_loop(
+                pages1, hv, tile1, pl_o, pl_h, False)), 4),
+        })
     b1 = n * S1 * tile1
     qwen = {"blocks": n, "extents_per_direction": n * S1, "bytes_per_direction": b1,
+            "swap_out_latency_wall": latency,
             "aegkv_ms": {"D2H": round(t_out, 3), "H2D": round(t_in, 3)},
             "reference_loop_ms": {"D2H": round(r_out, 3), "H2D": round(r_in, 3)},
             "aegkv_GBps": {"D2H": round(b1 / t_out / 1e6, 2), "H2D": round(b1 / t_in / 1e6, 2)},
@@ -591,6 +620,7 @@ def main():
     in_ids = rest[torch.randperm(rest.size, generator=g)[:NSW].numpy()]
     common1 = ([tile1] * S1, [s * tile1 for s in range(S1)], [1] * S1, NB1, [1], pool.tensor,
                S1 * tile1, 0)
+    lay = ops.SegmentLayout(segs1, *common1)
     zero = np.zeros(NSW, np.int32)
     ones = np.ones(NSW, np.int64)
     swap_bytes = NSW * S1 * tile1
@@ -608,11 +638,9 @@ def main():
 
     def step(evs):
         evs[0].record()
-        ops.swap_segments(segs1, *common1, out_ids, host_ids, zero, zero, ones, False,
-                          mode=args.mode)
+        lay.swap(out_ids, host_ids, zero, zero, ones, False, mode=args.mode)
         evs[1].record()
-        ops.swap_segments(segs1, *common1, host_ids, in_ids, zero, zero, ones, True,
-                          mode=args.mode)
+        lay.swap(host_ids, in_ids, zero, zero, ones, True, mode=args.mode)
         evs[2].record()
         ops.copy_blocks(segs2, csrc, cdst)
         evs[3].record()

@@ -128,6 +128,57 @@ def test_seeded_swap_vs_oracle(gpu, oracle, seed, mode):
     pool.free()
 
 
+def test_prepared_layout_reused_across_calls_vs_oracle(gpu, oracle):
+    """One SegmentLayout serves a sequence of calls of varying size, both
+    directions and both modes (including an empty call); after each call the
+    device and host bytes equal the oracle's state."""
+    rng = np.random.default_rng(21)
+    kpp, page, owners, cpu_off = _random_layout(rng)
+    composite = int(page.sum())
+    n_gpu, n_host = 40, 36
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    host_np = rng.integers(0, 256, (n_host, composite), dtype=np.uint8)
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    pool = _pool_from(host_np)
+    lay = ops.SegmentLayout(segs, page, cpu_off, owners, n_gpu, kpp, pool.tensor, composite, 0)
+    for step, (n, is_in, mode) in enumerate([(30, False, "direct"), (0, True, "staged"),
+                                              (7, True, "staged"), (1, False, "staged"),
+                                              (25, True, "direct"), (3, False, "auto")]):
+        _say("prepared layout step", step, "n", n, "swap_in", is_in, mode)
+        grp = rng.integers(0, 3, n).astype(np.int32)
+        first = np.array([rng.integers(0, kpp[g] + 1) for g in grp], np.int64)
+        valid = np.array([rng.integers(0, kpp[g] - f + 1) for g, f in zip(grp, first)],
+                         np.int64)
+        dev_ids = rng.permutation(n_gpu)[:n]
+        host_ids = rng.permutation(n_host)[:n]
+        src, dst = (host_ids, dev_ids) if is_in else (dev_ids, host_ids)
+        lay.swap(src, dst, grp, first, valid, is_in, mode=mode)
+        oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu,
+                           kpp, host_np.reshape(-1), composite, 0, composite, src, dst, grp,
+                           first, valid, is_in)
+        torch.cuda.synchronize()
+        assert np.array_equal(pool.tensor.numpy().reshape(host_np.shape), host_np), step
+        for s in range(len(page)):
+            assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (step, s)
+    del lay
+    pool.free()
+
+
+def test_prepared_layout_rejects_bad_geometry(gpu):
+    seg = torch.zeros(8, 256, dtype=torch.uint8, device=gpu)
+    pool = ops.PinnedHostPool(4 * 256)
+    with pytest.raises(ValueError, match="holds"):
+        ops.SegmentLayout([seg], [256], [0], [1], 9, [1], pool.tensor, 256, 0)
+    with pytest.raises(ValueError, match="lengths"):
+        ops.SegmentLayout([seg], [256, 256], [0], [1], 8, [1], pool.tensor, 256, 0)
+    with pytest.raises(ValueError, match="host tensor"):
+        ops.SegmentLayout([seg], [256], [0], [1], 8, [1], seg.view(-1), 256, 0)
+    lay = ops.SegmentLayout([seg], [256], [0], [1], 8, [1], pool.tensor, 256, 0)
+    with pytest.raises(ValueError, match="equal lengths"):
+        lay.swap([1], [0], [0, 0], [0], [1], False)
+    pool.free()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_unaligned_host_pool_vs_oracle(gpu, oracle, mode):
     """A host pool starting 1 byte into its allocation forces the

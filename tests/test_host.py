@@ -7,6 +7,7 @@ from pathlib import Path
 
 import numpy as np
 import pytest
+import torch
 
 from aegaeon_amd import cache_transfer as ct
 from aegaeon_amd.cache_groups import (
@@ -236,6 +237,18 @@ def test_early_validation_without_gpu(aegkv_lib):
         _lib.check(rc)
     assert lib.aegkv_host_alloc(None, 16) == _lib.EINVAL
     assert lib.aegkv_host_free(None) == 0
+
+
+def test_prepared_layout_rejects_host_segments():
+    """SegmentLayout checks its tensors before it touches the library."""
+    from aegaeon_amd import ops
+
+    seg = torch.zeros(4, 64, dtype=torch.uint8)
+    pool = torch.zeros(4 * 64, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="device"):
+        ops.SegmentLayout([seg], [64], [0], [1], 4, [1], pool, 64, 0)
+    with pytest.raises(ValueError, match="at least one"):
+        ops.SegmentLayout([], [], [], [], 4, [1], pool, 64, 0)
 
 
 def test_tuning_knobs(aegkv_lib):
