@@ -3,19 +3,24 @@
 Synchronous mirror of the planning half of the reference's BlockManager:
 the GPU free lists (aegaeon/block_manager.py:718-793, 956-974), the CPU slab
 allocator (:653-659, 976-1029), the move planner of move_requests
-(:1355-1478) and the reclamation of a finished move's source blocks
-(:663-690). Ray RPC, asyncio waits and CUDA events are not part of it: a
-caller runs the returned SwapPlan through KVSwapper.swap_blocks (or the C
-ABI) and calls BlockPools.reclaim(plan) once the move's event has completed.
+(:1355-1478), the move-event ledger (:518-563, 1498-1518) and the
+reclamation of finished moves' source blocks (:661-690, 804-939). Ray RPC is
+not part of it: a caller runs the returned SwapPlan through
+KVSwapper.swap_blocks (or the C ABI) and either records the move with the
+event that call returns (BlockPools.record_move; the ids come back when the
+event has completed, in move order) or calls BlockPools.reclaim(plan) itself
+once the move is known to be done. Where the reference awaits an event in an
+asyncio task, this code polls it (query) or blocks on it (synchronize).
 """
 
 from __future__ import annotations
 
 import ctypes
+import itertools
 import math
 from collections import defaultdict, deque
 from dataclasses import dataclass, field
-from typing import Deque, Dict, List, Optional, Sequence, Tuple
+from typing import Callable, Deque, Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 
@@ -53,15 +58,32 @@ class BlockPools:
         self.gpu_free_blocks: Dict[int, List[int]] = {}
         self.gpu_block_shape: Dict[int, Tuple[int, ...]] = {}
         self.gpu_cache_groups: Dict[int, Tuple[CacheGroupConfig, ...]] = {}
+        # moves whose source ids are not free yet: swap-outs by source engine,
+        # swap-ins by host block shape (block_manager.py:619-636)
+        self._serial = itertools.count()
+        self.move_events_gpu: Dict[int, Deque["MoveRecord"]] = defaultdict(deque)
+        self.move_gpu_num_blocks: Dict[int, int] = defaultdict(int)
+        self.move_events_cpu: Dict[Tuple[int, ...], Deque["MoveRecord"]] = defaultdict(deque)
+        self.move_cpu_num_blocks: Dict[Tuple[int, ...], int] = defaultdict(int)
 
     def block_size_bytes(self, block_shape: Tuple[int, ...]) -> int:
         return math.prod(block_shape) * self.dtype_size
 
     def register_gpu_space(self, engine_id: int, num_max_blocks: int,
                            block_shape: Tuple[int, ...],
-                           cache_groups: Sequence[CacheGroupConfig]) -> None:
+                           cache_groups: Sequence[CacheGroupConfig],
+                           block_tables: Optional[Dict[int, BlockTable]] = None) -> None:
         """Expose device ids 1..num_max_blocks-1 (block 0 is vLLM's null
-        block), as block_manager.py:775-792 does."""
+        block), as block_manager.py:775-792 does.
+
+        Registering an engine again replaces its cache space
+        (block_manager.py:718-761): no request in `block_tables` may still
+        reside there, the engine's pending swap-outs are dropped (its free
+        list is rebuilt whole) and the host ids of swap-ins into the old
+        space are freed at once, since a model switch has already waited for
+        every move into it. The arguments are checked before any state
+        changes.
+        """
         if num_max_blocks <= 1:
             raise ValueError(
                 "GPU cache must contain at least one usable block in addition to the "
@@ -69,6 +91,26 @@ class BlockPools:
             )
         if not cache_groups:
             raise ValueError("GPU cache must expose at least one cache group")
+        if engine_id in self.gpu_free_blocks and block_tables is not None:
+            for rid, table in block_tables.items():
+                if table.location == engine_id:
+                    raise ValueError(
+                        f"Error registering new GPU cache space for engine_id {engine_id}; "
+                        f"Request #{rid} still resides in the cache."
+                    )
+        self.move_events_gpu.pop(engine_id, None)
+        self.move_gpu_num_blocks[engine_id] = 0
+        old_shape = self.gpu_block_shape.get(engine_id)
+        if old_shape is not None:
+            pending = self.move_events_cpu[old_shape]
+            keep = deque()
+            for rec in pending:
+                if rec.plan.target_location == engine_id:
+                    self._reclaim_record(rec)
+                else:
+                    keep.append(rec)
+            pending.clear()
+            pending.extend(keep)
         self.gpu_block_shape[engine_id] = tuple(block_shape)
         self.gpu_cache_groups[engine_id] = tuple(cache_groups)
         self.gpu_free_blocks[engine_id] = list(range(VLLM_NULL_BLOCK_ID + 1, num_max_blocks))
@@ -100,6 +142,9 @@ class BlockPools:
                 raise KeyError(f"unknown gpu location {location}")
             free = self.gpu_free_blocks[location]
             if len(free) < num_blocks:
+                # wait for this engine's swap-outs and take back their sources
+                self.reclaim_gpu_moves(location, wait=True)
+            if len(free) < num_blocks:
                 raise ResourceWarning(
                     f"not enough free blocks on GPU, requested {num_blocks}, "
                     f"available {len(free)}"
@@ -109,6 +154,10 @@ class BlockPools:
             return out
         block_bytes = self.block_size_bytes(block_shape)
         free = self.cpu_free_blocks[block_shape]
+        if not self._cpu_blocks_available(block_bytes, num_blocks - len(free)):
+            # wait for swap-ins of this shape, free their host ids and any
+            # slab left empty (which may shrink `free`)
+            self.reclaim_cpu_moves(block_shape, wait=True)
         if not self._cpu_blocks_available(block_bytes, num_blocks - len(free)):
             raise ResourceWarning(
                 f"not enough free blocks on CPU, requested {num_blocks}, available "
@@ -142,6 +191,113 @@ class BlockPools:
         """Free a completed move's source ids (all of them, including pages
         that were not copied)."""
         self.release(plan.release_source_block_ids, plan.source_location, plan.block_shape)
+
+    # ------------------------------------------------------ move ledger --
+
+    def record_move(self, plan: "SwapPlan", events: Sequence,
+                    finished: Optional[Callable[[], bool]] = None) -> "MoveRecord":
+        """Remember a submitted move until its events complete
+        (block_manager.py:1498-1518).
+
+        events: one completion event per worker that runs the move (objects
+        with query() -> bool and synchronize(), e.g. the torch.cuda.Event
+        KVSwapper.swap_blocks returns). finished: optional predicate that is
+        true once every request of the move has finished, after which the
+        move counts as done without looking at its events.
+        """
+        rec = MoveRecord(next(self._serial), plan, list(events), finished)
+        n = len(plan.release_source_block_ids)
+        if is_gpu(plan.source_location):
+            self.move_gpu_num_blocks[plan.source_location] += n
+            self.move_events_gpu[plan.source_location].append(rec)
+        else:
+            self.move_cpu_num_blocks[plan.block_shape] += n
+            self.move_events_cpu[plan.block_shape].append(rec)
+        return rec
+
+    def _reclaim_record(self, rec: "MoveRecord") -> int:
+        """Return one finished move's source ids (block_manager.py:661-690)."""
+        plan = rec.plan
+        n = len(plan.release_source_block_ids)
+        if is_gpu(plan.source_location):
+            self.move_gpu_num_blocks[plan.source_location] -= n
+        else:
+            self.move_cpu_num_blocks[plan.block_shape] -= n
+        self.release(plan.release_source_block_ids, plan.source_location, plan.block_shape)
+        return n
+
+    def _reclaim_queue(self, queue: Deque["MoveRecord"], wait: bool) -> Tuple[int, int]:
+        """Reclaim moves in the order they were recorded, up to the newest
+        one present at the call (block_manager.py:804-851). With wait, block
+        on each move's events; without, stop at the first move still
+        running. Returns (moves, blocks) reclaimed."""
+        if not queue:
+            return 0, 0
+        target = queue[-1].serial
+        moves = blocks = 0
+        while queue and queue[0].serial <= target:
+            rec = queue[0]
+            if wait:
+                rec.wait()
+            elif not rec.done():
+                break
+            queue.popleft()
+            moves += 1
+            blocks += self._reclaim_record(rec)
+        return moves, blocks
+
+    def reclaim_gpu_moves(self, location: int, wait: bool = True) -> Tuple[int, int]:
+        """Free the source ids of engine `location`'s swap-outs
+        (block_manager.py:853-880)."""
+        return self._reclaim_queue(self.move_events_gpu[location], wait)
+
+    def reclaim_cpu_moves(self, block_shape: Tuple[int, ...],
+                          wait: bool = True) -> Tuple[int, int]:
+        """Free the host ids of swap-ins of `block_shape`, then every slab
+        left empty (block_manager.py:882-916)."""
+        got = self._reclaim_queue(self.move_events_cpu[tuple(block_shape)], wait)
+        self.reclaim_cpu_slabs()
+        return got
+
+    def reclaim_cpu_slabs(self) -> int:
+        """Give slabs with no used block back to the free slab list and drop
+        their ids from the shape's free deque (block_manager.py:918-939)."""
+        reclaimed = 0
+        for slab, usage in enumerate(self.cpu_slab_usage):
+            shape = self.cpu_block_shape[slab]
+            if usage != 0 or shape is None:
+                continue
+            lo, hi = slab_range(slab, self.cpu_slab_size_bytes, self.block_size_bytes(shape))
+            free = self.cpu_free_blocks[shape]
+            kept = [b for b in free if not lo <= b < hi]
+            free.clear()
+            free.extend(kept)
+            self.cpu_free_slabs.append(slab)
+            self.cpu_block_shape[slab] = None
+            reclaimed += 1
+        return reclaimed
+
+
+@dataclass
+class MoveRecord:
+    """One submitted move whose source ids are not free yet
+    (MoveEvent, block_manager.py:518-563)."""
+
+    serial: int
+    plan: "SwapPlan"
+    events: List
+    finished: Optional[Callable[[], bool]] = None
+
+    def done(self) -> bool:
+        if self.finished is not None and self.finished():
+            return True
+        return all(ev.query() for ev in self.events)
+
+    def wait(self) -> None:
+        if self.finished is not None and self.finished():
+            return
+        for ev in self.events:
+            ev.synchronize()
 
 
 _KIND = {"attention": 0, "mamba_none": 1}
@@ -293,4 +449,5 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
     return plan
 
 
-__all__ = ["BLOCK_LOCATION_CPU", "BlockPools", "SwapPlan", "plan_move", "slab_range"]
+__all__ = ["BLOCK_LOCATION_CPU", "BlockPools", "MoveRecord", "SwapPlan", "plan_move",
+           "slab_range"]

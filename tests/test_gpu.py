@@ -179,6 +179,52 @@ def test_prepared_layout_rejects_bad_geometry(gpu):
     pool.free()
 
 
+def test_threads_swap_concurrently_on_their_own_streams(gpu):
+    """Four host threads share one layout (and the library's descriptor ring
+    and DMA streams) and swap out, each on its own stream, alternating
+    DIRECT and STAGED; every call lands its own blocks in its own host pages."""
+    import threading
+
+    n_gpu, page, n, n_thr, iters = 64, 8192, 16, 4, 40
+    segs = [torch.randint(0, 256, (n_gpu, page), dtype=torch.uint8, device=gpu)
+            for _ in range(3)]
+    segs_cpu = [x.cpu() for x in segs]
+    pool = ops.PinnedHostPool(n_thr * n * 3 * page)
+    lay = ops.SegmentLayout(segs, [page] * 3, [0, page, 2 * page], [1, 1, 1], n_gpu, [1],
+                            pool.tensor, 3 * page, 0)
+    host = pool.tensor.view(n_thr * n, 3, page)
+    errors = []
+
+    def worker(t):
+        try:
+            st = torch.cuda.Stream(gpu)
+            rng = np.random.default_rng(t)
+            dst = t * n + np.arange(n)
+            for it in range(iters):
+                src = rng.permutation(n_gpu)[:n]
+                lay.swap(src, dst, np.zeros(n, np.int32), np.zeros(n), np.ones(n), False,
+                         mode=MODES[it % 2], stream=st)
+                st.synchronize()
+                mine = host[t * n:(t + 1) * n]
+                idx = torch.from_numpy(src)
+                for s in range(3):
+                    if not torch.equal(mine[:, s], segs_cpu[s][idx]):
+                        errors.append((t, it, s))
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    _say("threads", n_thr, "iterations", iters)
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(n_thr)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads)
+    assert errors == []
+    del lay
+    pool.free()
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_unaligned_host_pool_vs_oracle(gpu, oracle, mode):
     """A host pool starting 1 byte into its allocation forces the
@@ -505,14 +551,17 @@ def test_planner_swap_out_and_back_in(gpu):
     ev = sw.swap_blocks(out.request_ids, out.source_block_ids, out.target_block_ids,
                         out.group_ids, out.first_kernel_blocks, out.valid_kernel_blocks,
                         [None] * len(out.request_ids), False)
-    ev.synchronize()
-    pools.reclaim(out)
+    pools.record_move(out, [ev])          # device sources stay taken until ev completes
     back = plan_move(reqs, tables, 0, pools)
     ev2 = sw.swap_blocks(back.request_ids, back.source_block_ids, back.target_block_ids,
                          back.group_ids, back.first_kernel_blocks, back.valid_kernel_blocks,
                          [ev] * len(back.request_ids), True)
-    ev2.synchronize()
-    pools.reclaim(back)
+    pools.record_move(back, [ev2])
+    assert not set(back.target_block_ids) & set(out.release_source_block_ids)
+    assert pools.reclaim_cpu_moves(shape) == (1, len(back.release_source_block_ids))
+    assert ev2.query() and ev.query()
+    assert pools.reclaim_gpu_moves(0, wait=False) == (1, len(out.release_source_block_ids))
+    assert sum(pools.cpu_slab_usage) == 0 and len(pools.cpu_free_slabs) == 40
     owners = [(0, 0), (1, 1), (2, 0), (2, 1)]  # (backing tensor, group)
     pages = [2048, 2048, 4096]
     checked = 0

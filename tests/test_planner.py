@@ -182,3 +182,135 @@ def test_native_transfer_entries_rejections(aegkv_lib):
     with pytest.raises(ValueError):
         native_transfer_entries(GROUPS, [(t2, 10)])    # column lists per group missing
     assert native_transfer_entries(GROUPS, []) == []
+
+
+# ------------------------------------------------------------ move ledger --
+
+G1 = (CacheGroupConfig("attention", 16, 16),)
+
+
+class FakeEvent:
+    """A completion event the test finishes by hand."""
+
+    def __init__(self):
+        self.complete = False
+        self.waited = 0
+
+    def query(self):
+        return self.complete
+
+    def synchronize(self):
+        self.waited += 1
+        self.complete = True
+
+
+def _engine_with_requests(n_req, per_req, num_max_blocks=12, **pool_kw):
+    pools = BlockPools(**(pool_kw or dict(cpu_num_slabs=8, cpu_slab_size_bytes=1 << 16)))
+    pools.register_gpu_space(0, num_max_blocks, SHAPE, G1)
+    tables = {rid: BlockTable(0, SHAPE, G1, [pools.allocate(per_req, 0, SHAPE)])
+              for rid in range(n_req)}
+    return pools, tables
+
+
+def test_move_ledger_reclaims_in_record_order():
+    """Source ids return only when the move's event has completed, and in
+    the order moves were recorded (block_manager.py:804-851)."""
+    pools, tables = _engine_with_requests(2, 4)
+    assert pools.gpu_free_blocks[0] == [9, 10, 11]
+    p0 = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    p1 = plan_move([(1, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    e0, e1 = FakeEvent(), FakeEvent()
+    r0 = pools.record_move(p0, [e0])
+    r1 = pools.record_move(p1, [e1])
+    assert r0.serial < r1.serial
+    assert pools.move_gpu_num_blocks[0] == 8
+    e1.complete = True
+    assert pools.reclaim_gpu_moves(0, wait=False) == (0, 0)   # e0 still running
+    assert pools.gpu_free_blocks[0] == [9, 10, 11]
+    e0.complete = True
+    assert pools.reclaim_gpu_moves(0, wait=False) == (2, 8)
+    assert pools.gpu_free_blocks[0] == [9, 10, 11, 1, 2, 3, 4, 5, 6, 7, 8]
+    assert pools.move_gpu_num_blocks[0] == 0
+    assert e0.waited == e1.waited == 0
+    assert pools.reclaim_gpu_moves(0) == (0, 0)
+
+
+def test_gpu_allocation_waits_for_swap_outs():
+    """A GPU allocation the free list cannot serve waits for the engine's
+    swap-outs and takes back their sources (block_manager.py:956-970)."""
+    pools, tables = _engine_with_requests(2, 4)
+    p0 = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    e0 = FakeEvent()
+    pools.record_move(p0, [e0])
+    assert pools.allocate(3, 0, SHAPE) == [9, 10, 11]       # no wait needed
+    assert e0.waited == 0
+    assert pools.allocate(2, 0, SHAPE) == [1, 2]            # waits on the swap-out
+    assert e0.waited == 1
+    with pytest.raises(ResourceWarning):
+        pools.allocate(3, 0, SHAPE)
+
+
+def test_finished_requests_end_their_move():
+    pools, tables = _engine_with_requests(1, 4)
+    p0 = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    never = FakeEvent()
+    pools.record_move(p0, [never], finished=lambda: True)
+    assert pools.reclaim_gpu_moves(0, wait=False) == (1, 4)
+    assert never.waited == 0
+
+
+def test_swap_in_reclaim_frees_host_ids_and_empty_slabs():
+    pools, tables = _engine_with_requests(1, 4)
+    out = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    pools.record_move(out, [FakeEvent()])
+    used = [s for s, u in enumerate(pools.cpu_slab_usage) if u]
+    assert len(used) == 1 and pools.cpu_slab_usage[used[0]] == 4
+    back = plan_move([(0, 64)], tables, 0, pools)             # allocates 4 GPU ids
+    e = FakeEvent()
+    pools.record_move(back, [e])
+    assert pools.move_cpu_num_blocks[SHAPE] == 4
+    assert pools.reclaim_cpu_moves(SHAPE, wait=False) == (0, 0)
+    e.complete = True
+    assert pools.reclaim_cpu_moves(SHAPE, wait=False) == (1, 4)
+    assert sum(pools.cpu_slab_usage) == 0
+    assert sorted(pools.cpu_free_slabs) == list(range(8))
+    assert len(pools.cpu_free_blocks[SHAPE]) == 0
+    assert all(s is None for s in pools.cpu_block_shape)
+
+
+def test_cpu_allocation_waits_for_swap_ins():
+    """One slab of exactly four host blocks: a second swap-out must wait for
+    the swap-in that still reads the first request's host pages."""
+    pools, tables = _engine_with_requests(2, 4, num_max_blocks=16, cpu_num_slabs=1,
+                                          cpu_slab_size_bytes=8000)
+    out = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    pools.reclaim(out)
+    back = plan_move([(0, 64)], tables, 0, pools)
+    e = FakeEvent()
+    pools.record_move(back, [e])
+    out1 = plan_move([(1, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    assert e.waited == 1
+    assert sorted(out1.target_block_ids) == [0, 1, 2, 3]
+
+
+def test_reregistering_an_engine_settles_its_moves():
+    pools, tables = _engine_with_requests(2, 4)
+    with pytest.raises(ValueError, match="still resides"):
+        pools.register_gpu_space(0, 12, SHAPE, G1, block_tables=tables)
+    out = plan_move([(0, 64), (1, 64)], tables, BLOCK_LOCATION_CPU, pools)
+    pools.record_move(out, [FakeEvent()])
+    back = plan_move([(0, 64)], tables, 0, pools)
+    e = FakeEvent()
+    pools.record_move(back, [e])
+    with pytest.raises(ValueError):
+        pools.register_gpu_space(0, 1, SHAPE, G1)     # rejected before any change
+    assert pools.move_cpu_num_blocks[SHAPE] == 4
+    again = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)   # switch away
+    pools.record_move(again, [FakeEvent()])
+    assert sum(pools.cpu_slab_usage) == 12
+    pools.register_gpu_space(0, 20, SHAPE, G1, block_tables=tables)
+    assert e.waited == 0                               # freed without waiting
+    assert pools.move_cpu_num_blocks[SHAPE] == 0
+    assert len(pools.move_events_gpu[0]) == 0 and pools.move_gpu_num_blocks[0] == 0
+    assert pools.gpu_free_blocks[0] == list(range(1, 20))
+    assert sum(pools.cpu_slab_usage) == 8              # both requests on the host
