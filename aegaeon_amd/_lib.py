@@ -53,6 +53,8 @@ EXPORTED_SYMBOLS = (
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
     "aegkv_host_free",
+    "aegkv_fence_signal",
+    "aegkv_fence_wait",
 )
 
 _P = ctypes.c_void_p
@@ -82,6 +84,8 @@ _SIGNATURES = {
     ),
     "aegkv_host_alloc": (_INT, [_PP, _I64]),
     "aegkv_host_free": (_INT, [_P]),
+    "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
+    "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),
 }
 
 _lib = None

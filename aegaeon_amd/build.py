@@ -39,14 +39,15 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile csrc/aegkv.hip and csrc/plan.cpp into aegaeon_amd/libaegkv.so
-    (always rebuilds)."""
+    """Compile csrc/aegkv.hip, csrc/fence.hip and csrc/plan.cpp into
+    aegaeon_amd/libaegkv.so (always rebuilds)."""
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [
         hipcc(),
         *HIPCC_FLAGS,
         f"-I{REPO_DIR / 'include'}",
         str(CSRC / "aegkv.hip"),
+        str(CSRC / "fence.hip"),
         str(CSRC / "plan.cpp"),
         "-o",
         str(tmp),

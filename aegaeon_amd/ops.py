@@ -345,3 +345,61 @@ class PinnedHostPool:
     def free(self) -> None:
         """Drop this pool's reference; the memory goes once no view remains."""
         self.tensor = None
+
+
+def _fence_word(words: torch.Tensor, index: int, what: str) -> int:
+    if words.dtype != torch.int64 or words.dim() != 1:
+        raise ValueError(f"{what} must be a 1-D int64 tensor")
+    if not words.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if not 0 <= index < words.numel():
+        raise ValueError(f"{what} index {index} outside [0, {words.numel()})")
+    return words.data_ptr() + 8 * index
+
+
+def fence_signal(words: torch.Tensor, index: int, value: int, *,
+                 stream: torch.cuda.Stream | None = None) -> None:
+    """Raise words[index] to at least `value` once every operation enqueued
+    earlier on `stream` (default: the current stream) has finished
+    (aegkv_fence_signal). The counterpart of recording an interprocess event
+    behind a swap (aegaeon/worker.py:2331,2349).
+
+    words: a 1-D int64 tensor on the device, e.g. one shared with other
+    processes through torch.multiprocessing (a HIP IPC memory handle).
+    """
+    if not 0 < value < (1 << 63):
+        raise ValueError("fence values are positive and below 2**63")
+    ptr = _fence_word(words, index, "fence words")
+    dev = words.device
+    if dev.type != "cuda":
+        raise ValueError("fence words must live on the device")
+    lib = _lib.load()
+    with _OnDevice(dev):
+        rc = lib.aegkv_fence_signal(ptr, int(value), _stream_ptr(dev, stream))
+    _lib.check(rc)
+
+
+def fence_wait(words: torch.Tensor, index: int, value: int, timed_out: torch.Tensor,
+               timed_out_index: int = 0, *, timeout_s: float = 30.0,
+               stream: torch.cuda.Stream | None = None) -> None:
+    """Make every later operation on `stream` wait until words[index] >=
+    value (aegkv_fence_wait); the counterpart of waiting on another worker's
+    interprocess event (aegaeon/worker.py:2351-2394).
+
+    A wait that has polled for `timeout_s` seconds gives up, sets
+    timed_out[timed_out_index] to 1 and lets the stream go on; the flag is
+    never cleared here, so check it (after the stream has passed the wait)
+    before trusting what followed.
+    """
+    if not 0 < value < (1 << 63):
+        raise ValueError("fence values are positive and below 2**63")
+    ptr = _fence_word(words, index, "fence words")
+    flag = _fence_word(timed_out, timed_out_index, "timed_out")
+    dev = words.device
+    if dev.type != "cuda" or timed_out.device != dev:
+        raise ValueError("fence words and the timed_out flags must live on one device")
+    timeout_us = int(timeout_s * 1e6)
+    lib = _lib.load()
+    with _OnDevice(dev):
+        rc = lib.aegkv_fence_wait(ptr, int(value), timeout_us, flag, _stream_ptr(dev, stream))
+    _lib.check(rc)

@@ -7,20 +7,27 @@ wait_for_all_move_in/out (:2406-2418). The reference issues one
 torch copy_ per (segment, entry) extent from a Python double loop; here the
 whole list is one call into libaegkv.so, one kernel launch per call.
 
-A source event may be a local torch.cuda.Event or the IPC handle bytes
-another process exported (utils.py:263-288 reduce/rebuild_cuda_event). With
-interprocess_events=True the completion events are created interprocess-capable
-like the reference's (worker.py:2249) and event_ipc_handle() exports them;
-the default is local events, because the HIP runtime used here rejects
-recording interprocess events (hipErrorInvalidValue). Ray object refs are not
-part of this module.
+A source event may be a local torch.cuda.Event, the IPC handle bytes
+another process exported (utils.py:263-288 reduce/rebuild_cuda_event), or a
+FenceToken. With interprocess_events=True the completion events are created
+interprocess-capable like the reference's (worker.py:2249) and
+event_ipc_handle() exports them; the default is local events, because the
+HIP runtime used here rejects recording interprocess events
+(hipErrorInvalidValue). Ordering across processes therefore uses fences: a
+device int64 tensor of counters shared by the workers (fence_words), in
+which each swapper owns one word per swap stream (fence_slots). After each
+swap the swapper raises its word to the next count on that stream and
+publishes FenceToken(word, count) as last_fence; a swap in another process
+that lists the token among its source events waits on the device until the
+word has reached the count. Ray object refs are not part of this module.
 """
 
 from __future__ import annotations
 
 import logging
 from collections import defaultdict
-from typing import Dict, List, Optional, Sequence, Union
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 import torch
@@ -32,13 +39,26 @@ from .layout import CompositeCache, host_page_geometry
 logger = logging.getLogger("aegaeon_amd.swap")
 
 
+@dataclass(frozen=True)
+class FenceToken:
+    """Completion of a swap as a fence: the swap has finished once
+    fence_words[slot] >= value. Plain ints, so it crosses process
+    boundaries like the reference's event handle bytes."""
+
+    slot: int
+    value: int
+
+
 class KVSwapper:
     """Executes swap lists between a CompositeCache and a pinned host pool."""
 
     def __init__(self, cache: CompositeCache, group_layer_names: Sequence[set],
                  group_descriptors: Sequence[CacheGroupRuntimeConfig],
                  host_pool: torch.Tensor, tp_rank: int = 0, tp_size: int = 1,
-                 host_element_size: int = 2, interprocess_events: bool = False):
+                 host_element_size: int = 2, interprocess_events: bool = False,
+                 fence_words: Optional[torch.Tensor] = None,
+                 fence_slots: Optional[Tuple[int, int]] = None,
+                 fence_timeout_s: float = 30.0):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -99,6 +119,25 @@ class KVSwapper:
         self.swap_in_stream = torch.cuda.Stream(device)
         self.swap_out_stream = torch.cuda.Stream(device)
         self.move_event_table: Dict[int, List[torch.cuda.Event]] = defaultdict(list)
+        # fences: (swap-out word, swap-in word) this swapper raises; flags
+        # its waits set on timeout, [swap-out stream, swap-in stream]
+        if fence_slots is not None and fence_words is None:
+            raise ValueError("fence_slots need fence_words")
+        if fence_words is not None:
+            if fence_words.device != device:
+                raise ValueError("fence words must live on the cache's device")
+            if fence_slots is not None:
+                for w in fence_slots:
+                    if not 0 <= w < fence_words.numel():
+                        raise ValueError(f"fence slot {w} outside the fence words")
+                if fence_slots[0] == fence_slots[1]:
+                    raise ValueError("each swap stream needs its own fence word")
+        self.fence_words = fence_words
+        self.fence_slots = tuple(fence_slots) if fence_slots is not None else None
+        self.fence_timeout_s = fence_timeout_s
+        self._fence_count = [0, 0]
+        self._fence_timed_out = torch.zeros(2, dtype=torch.int64, device=device)
+        self.last_fence: Optional[FenceToken] = None
 
     def swap_blocks(self, request_ids: Sequence[int], source_block_ids: Sequence[int],
                     target_block_ids: Sequence[int], group_ids: Sequence[int],
@@ -132,16 +171,28 @@ class KVSwapper:
         new_event = torch.cuda.Event(interprocess=self.interprocess_events)
         # wait for in-flight moves of the same requests (worker.py:2351-2394);
         # bytes are IPC handles exported by another process
+        side = 1 if is_swap_in else 0
         for rid, ev in zip(request_ids, source_events):
             if ev is not None:
-                if isinstance(ev, (bytes, bytearray)):
-                    ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
-                stream.wait_event(ev)
+                if isinstance(ev, FenceToken):
+                    if self.fence_words is None:
+                        raise ValueError("a FenceToken source needs fence_words")
+                    ops.fence_wait(self.fence_words, ev.slot, ev.value, self._fence_timed_out,
+                                   side, timeout_s=self.fence_timeout_s, stream=stream)
+                else:
+                    if isinstance(ev, (bytes, bytearray)):
+                        ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
+                    stream.wait_event(ev)
             self.move_event_table[rid].append(new_event)
         self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
                           first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
                           stream=stream)
         new_event.record(stream)
+        if self.fence_slots is not None:
+            self._fence_count[side] += 1
+            ops.fence_signal(self.fence_words, self.fence_slots[side], self._fence_count[side],
+                             stream=stream)
+            self.last_fence = FenceToken(self.fence_slots[side], self._fence_count[side])
         if logger.isEnabledFor(logging.INFO):
             valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
             copied = int((valid * self._bytes_per_kb[groups]).sum()) if groups.size else 0
@@ -167,8 +218,19 @@ class KVSwapper:
         for rid in request_ids:
             self.clear_request_resource(rid)
 
+    def _check_fences(self, side: int, stream: torch.cuda.Stream) -> None:
+        with torch.cuda.stream(stream):
+            if int(self._fence_timed_out[side].item()):
+                self._fence_timed_out[side].zero_()
+                raise RuntimeError(
+                    f"a swap-{'in' if side else 'out'} waited {self.fence_timeout_s} s for a "
+                    "source fence that was never signalled; swaps after that wait may have "
+                    "read data before its producer wrote it")
+
     def wait_for_all_move_in(self) -> None:
         self.swap_in_stream.synchronize()
+        self._check_fences(1, self.swap_in_stream)
 
     def wait_for_all_move_out(self) -> None:
         self.swap_out_stream.synchronize()
+        self._check_fences(0, self.swap_out_stream)

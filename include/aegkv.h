@@ -187,6 +187,35 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
 int aegkv_host_alloc(void** ptr, int64_t bytes);
 int aegkv_host_free(void* ptr);
 
+/*
+ * Fences: ordering a stream after work enqueued on another stream, in this
+ * process or another one, without interprocess events. Replaces the
+ * reference's event chaining between workers: the producer records an
+ * interprocess CUDA event behind its swap and returns the handle
+ * (aegaeon/worker.py:2331,2349); the consumer opens it and makes its stream
+ * wait (aegaeon/worker.py:2351-2394 via aegaeon/utils.py:263-288 and
+ * aegaeon/cuda_wrapper.py:43-233). The HIP runtime here refuses to record
+ * interprocess events, so the same contract is kept with counters.
+ *
+ * A fence word is an 8-byte aligned uint64 in device memory (possibly opened
+ * from another process's IPC memory handle) or in mapped pinned host memory.
+ *
+ * aegkv_fence_signal: once every operation enqueued on `stream` before it
+ * has finished, raise *word to at least `value` (atomic max, release at
+ * system scope). Give each producing stream its own word and signal
+ * increasing values.
+ *
+ * aegkv_fence_wait: every operation enqueued on `stream` after this call
+ * runs after *word has reached `value` (acquire at system scope). The wait
+ * gives up after `timeout_us` microseconds (0 < timeout_us <= 600 s) of
+ * polling; it then stores 1 into *timed_out and lets the stream continue, so
+ * the caller must check *timed_out (it is never cleared by the library)
+ * before trusting what the stream produced after the wait.
+ */
+int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream);
+int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
+                     uint64_t* timed_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

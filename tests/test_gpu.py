@@ -759,8 +759,9 @@ def _ipc_producer(q_in, q_out):
 
 
 @pytest.mark.skip(reason="the HIP runtime here rejects recording interprocess events "
-                         "(torch.cuda.Event(interprocess=True).record -> hipErrorInvalidValue), "
-                         "so cross-process event ordering cannot be exercised on this GPU")
+                         "(torch.cuda.Event(interprocess=True).record -> hipErrorInvalidValue); "
+                         "cross-process ordering is covered by fences instead "
+                         "(test_swap_waits_on_fence_from_another_process)")
 def test_swap_waits_on_ipc_event_from_another_process(gpu):
     """A source event exported by another process orders the swap after that
     process's write (worker.py:2351-2394)."""
@@ -793,6 +794,139 @@ def test_swap_waits_on_ipc_event_from_another_process(gpu):
         assert bool((got == 0x2B).all()), "swap ran before the other process's write"
         handle2 = KVSwapper.event_ipc_handle(ev)
         assert isinstance(handle2, (bytes, bytearray)) and len(handle2) > 0
+    finally:
+        q_in.put(None)
+        child.join(60)
+        if child.is_alive():
+            child.kill()
+    pool.free()
+
+
+# ------------------------------------------------------------------ fences --
+
+def _busy(n_iter=200):
+    """Keep the current stream busy for a while (bounded elementwise work)."""
+    busy = torch.zeros(1 << 26, dtype=torch.float32, device="cuda")
+    for _ in range(n_iter):
+        busy.add_(1.0)
+
+
+def test_fence_orders_a_swap_after_another_streams_write(gpu):
+    """Stream A writes the blocks late and signals; stream B waits on the
+    fence, then swaps the blocks out: B sees A's bytes, not the zeros that
+    were there when B's work was enqueued."""
+    n, page = 16, 65536
+    words = torch.zeros(4, dtype=torch.int64, device=gpu)
+    flags = torch.zeros(2, dtype=torch.int64, device=gpu)
+    seg = torch.zeros(n, page, dtype=torch.uint8, device=gpu)
+    pool = ops.PinnedHostPool(n * page)
+    pool.tensor.fill_(1)
+    lay = ops.SegmentLayout([seg], [page], [0], [1], n, [1], pool.tensor, page, 0)
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(a):
+        _busy()
+        seg.fill_(0x5A)
+        ops.fence_signal(words, 1, 7)
+    ops.fence_wait(words, 1, 7, flags, 0, timeout_s=30, stream=b)
+    lay.swap(np.arange(n), np.arange(n)[::-1].copy(), np.zeros(n, np.int32), np.zeros(n),
+             np.ones(n), False, stream=b)
+    b.synchronize()
+    assert int(flags[0]) == 0
+    assert bool((pool.tensor == 0x5A).all()), "the swap ran before the fence was signalled"
+    assert int(words[1]) == 7
+    ops.fence_signal(words, 1, 3)          # atomic max: a smaller value leaves it
+    torch.cuda.synchronize()
+    assert int(words[1]) == 7
+    del lay
+    pool.free()
+
+
+def test_fence_wait_gives_up_after_its_budget(gpu):
+    """An unsignalled fence ends the wait after the timeout, sets the flag,
+    and the swapper reports it once and clears it."""
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import FenceToken, KVSwapper
+
+    words = torch.zeros(4, dtype=torch.int64, device=gpu)
+    flags = torch.zeros(2, dtype=torch.int64, device=gpu)
+    st = torch.cuda.Stream()
+    ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0.002, stream=st)
+    st.synchronize()
+    assert flags.tolist() == [0, 1]
+    with pytest.raises(ValueError, match="timeout"):
+        ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0, stream=st)
+    with pytest.raises(ValueError, match="index"):
+        ops.fence_signal(words, 4, 1)
+
+    n_blocks, page = 8, 4096
+    cache = allocate_composite_cache([KVCacheTensorSpec(n_blocks * page, ("l0",))], n_blocks, gpu)
+    pool = ops.PinnedHostPool(4 * page)
+    sw = KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
+                   fence_words=words, fence_slots=(0, 1), fence_timeout_s=0.002)
+    sw.swap_blocks([1], [2], [0], [0], [0], [1], [FenceToken(3, 9)], False)
+    assert sw.last_fence == FenceToken(0, 1)
+    with pytest.raises(RuntimeError, match="never signalled"):
+        sw.wait_for_all_move_out()
+    sw.wait_for_all_move_out()             # reported once, then cleared
+    assert int(words[0]) == 1              # the swap still signalled its own word
+    pool.free()
+
+
+def _fence_producer(q_in, q_out):
+    """Child process: open the parent's fence words and cache blocks, then,
+    when told, write a pattern late and signal the fence behind it."""
+    import torch
+
+    from aegaeon_amd import ops as child_ops
+
+    words, pages = q_in.get()
+    torch.cuda.set_device(0)
+    q_out.put("ready")
+    assert q_in.get() == "go"
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        _busy(400)
+        pages[3:7].fill_(0x2B)
+        child_ops.fence_signal(words, 4, 1)
+    st.synchronize()
+    q_out.put("done")
+    q_in.get()  # keep the shared tensors open until the parent is done
+
+
+def test_swap_waits_on_fence_from_another_process(gpu):
+    """A FenceToken from another process orders the swap after that
+    process's write (the reference's cross-worker event wait,
+    worker.py:2351-2394): the swap is enqueued before the child writes."""
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import FenceToken, KVSwapper
+
+    _say("fence ordering across processes")
+    n_blocks, page = 16, 65536
+    cache = allocate_composite_cache([KVCacheTensorSpec(n_blocks * page, ("l0",))], n_blocks, gpu)
+    words = torch.zeros(8, dtype=torch.int64, device=gpu)
+    pool = ops.PinnedHostPool(4 * page)
+    pool.tensor.zero_()
+    sw = KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
+                   fence_words=words, fence_slots=(0, 1), fence_timeout_s=60)
+    torch.cuda.synchronize()
+    mp = torch.multiprocessing.get_context("spawn")
+    q_in, q_out = mp.Queue(), mp.Queue()
+    child = mp.Process(target=_fence_producer, args=(q_in, q_out), daemon=True)
+    child.start()
+    try:
+        q_in.put((words, cache.segment_pages(0)))
+        assert q_out.get(timeout=100) == "ready"
+        sw.swap_blocks([7], [3, 4, 5, 6], [0, 1, 2, 3], [0] * 4, [0] * 4, [1] * 4,
+                       [FenceToken(4, 1)], False)
+        q_in.put("go")
+        sw.wait_for_all_move_out()
+        assert q_out.get(timeout=100) == "done"
+        got = pool.tensor.view(4, page)
+        assert bool((got == 0x2B).all()), "the swap ran before the other process's write"
+        assert sw.last_fence == FenceToken(0, 1) and int(words[0]) == 1
     finally:
         q_in.put(None)
         child.join(60)

@@ -251,6 +251,26 @@ def test_prepared_layout_rejects_host_segments():
         ops.SegmentLayout([], [], [], [], 4, [1], pool, 64, 0)
 
 
+def test_fence_rejections_before_any_hip_call(aegkv_lib):
+    from aegaeon_amd import _lib
+
+    lib = aegkv_lib
+    assert lib.aegkv_fence_signal(None, 1, None) == _lib.EINVAL
+    assert lib.aegkv_fence_signal(0x1004, 1, None) == _lib.EINVAL       # not 8-byte aligned
+    assert b"aligned" in lib.aegkv_last_error()
+    assert lib.aegkv_fence_wait(0x1000, 1, 0, 0x2000, None) == _lib.ERANGE
+    assert lib.aegkv_fence_wait(0x1000, 1, 601 * 10**6, 0x2000, None) == _lib.ERANGE
+    assert lib.aegkv_fence_wait(None, 1, 1000, 0x2000, None) == _lib.EINVAL
+    from aegaeon_amd import ops
+
+    with pytest.raises(ValueError, match="int64"):
+        ops.fence_signal(torch.zeros(4, dtype=torch.int32), 0, 1)
+    with pytest.raises(ValueError, match="device"):
+        ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 1)
+    with pytest.raises(ValueError, match="positive"):
+        ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 0)
+
+
 def test_tuning_knobs(aegkv_lib):
     from aegaeon_amd import _lib
 
