@@ -83,9 +83,14 @@ struct Tunables {
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
+  // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
+  // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
+  // 32-160 KiB tiles; 16 KiB items lose 14 % at one per CU, so they keep 0).
+  int64_t copy_lds_bytes = int64_t(96) << 10;
 };
 Tunables g_tune;
 std::mutex g_tune_mu;
+constexpr int64_t kMaxLdsPerWorkgroup = int64_t(160) << 10;  // gfx950: 160 KiB per CU
 
 Tunables tunables() {
   std::lock_guard<std::mutex> lk(g_tune_mu);
@@ -510,22 +515,24 @@ hipError_t launch_swap(ShapeSel sh, bool to_host, bool vec, bool nt, int64_t gri
   return hipErrorInvalidValue;
 }
 
+// `lds`: dynamic LDS reserved per workgroup. The kernel does not use it; it
+// caps how many workgroups share a CU.
 template <int WG, int U, bool VEC, bool NT>
-hipError_t launch_copy_t(int64_t grid, hipStream_t st, const SegDesc* s, const PairDesc* p,
-                         uint32_t ns, uint32_t items, uint32_t cpt) {
+hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const SegDesc* s,
+                         const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
   hipLaunchKernelGGL((copy_blocks_kernel<WG, U, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(WG), 0, st, s, p, ns, items, cpt);
+                     dim3(WG), lds, st, s, p, ns, items, cpt);
   return hipGetLastError();
 }
 
-hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, hipStream_t st,
-                       const SegDesc* s, const PairDesc* p, uint32_t ns, uint32_t items,
-                       uint32_t cpt) {
-  if (!vec) return launch_copy_t<256, 1, false, false>(grid, st, s, p, ns, items, cpt);
-#define AEGKV_CP(W, UU)                                                          \
-  if (sh.wg == W && sh.u == UU)                                                  \
-    return nt ? launch_copy_t<W, UU, true, true>(grid, st, s, p, ns, items, cpt) \
-              : launch_copy_t<W, UU, true, false>(grid, st, s, p, ns, items, cpt);
+hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, unsigned lds,
+                       hipStream_t st, const SegDesc* s, const PairDesc* p, uint32_t ns,
+                       uint32_t items, uint32_t cpt) {
+  if (!vec) return launch_copy_t<256, 1, false, false>(grid, 0, st, s, p, ns, items, cpt);
+#define AEGKV_CP(W, UU)                                                               \
+  if (sh.wg == W && sh.u == UU)                                                       \
+    return nt ? launch_copy_t<W, UU, true, true>(grid, lds, st, s, p, ns, items, cpt) \
+              : launch_copy_t<W, UU, true, false>(grid, lds, st, s, p, ns, items, cpt);
   AEGKV_CP(256, 1) AEGKV_CP(256, 2) AEGKV_CP(256, 4)
   AEGKV_CP(1024, 1) AEGKV_CP(1024, 2) AEGKV_CP(1024, 3) AEGKV_CP(1024, 4)
   AEGKV_CP(1024, 5) AEGKV_CP(1024, 6) AEGKV_CP(1024, 8) AEGKV_CP(1024, 10)
@@ -931,6 +938,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
     case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
     case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
+    case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -949,6 +957,9 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "copy unroll must be 0 (auto) or one of 1,2,3,4,5,6,8,10");
     if (key == AEGKV_TUNE_STAGED_DMA_STREAMS && value > kMaxDmaStreams)
       return fail(AEGKV_EINVAL, "staged DMA streams must be in [0, %d]", kMaxDmaStreams);
+    if (key == AEGKV_TUNE_COPY_LDS_BYTES && value > kMaxLdsPerWorkgroup)
+      return fail(AEGKV_EINVAL, "copy LDS reservation must be in [0, %lld]",
+                  static_cast<long long>(kMaxLdsPerWorkgroup));
     if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
     *slot = value;
@@ -1077,7 +1088,10 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
   e = launch_copy(sh, vec, t.nt_stores != 0,
-                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg), stream,
+                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg),
+                  sh.wg == 1024 && sh.chunk() >= (int64_t(32) << 10)
+                      ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
+                  stream,
                   reinterpret_cast<const SegDesc*>(dv),
                   reinterpret_cast<const PairDesc*>(dv + pair_off),
                   static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),

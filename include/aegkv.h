@@ -66,6 +66,10 @@ extern "C" {
 #define AEGKV_TUNE_STAGED_DMA_STREAMS 10 /* STAGED copies fan out over this
                                           many library streams (0-4; <= 1:
                                           all on the caller's stream)     */
+#define AEGKV_TUNE_COPY_LDS_BYTES 11 /* copy_blocks, 1024-lane shapes with
+                                        >= 32 KiB items: LDS bytes reserved
+                                        per workgroup (0 - 160 KiB; caps
+                                        workgroups per CU; default 96 KiB) */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -7,6 +7,8 @@ host pages equal to the device tiles they came from, untouched blocks
 unchanged.
 """
 
+import itertools
+
 import numpy as np
 import pytest
 import torch
@@ -281,7 +283,7 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
 def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
-            _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES)
+            _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -289,24 +291,26 @@ def restore_tuning():
 
 
 def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
-    """Every instantiated copy shape and both grid policies, on tiles that
+    """Every instantiated copy shape, both grid policies and three LDS
+    reservations (none, one workgroup per CU, the whole LDS), on tiles that
     divide evenly, leave tails, or are smaller than one row."""
     rng = np.random.default_rng(21)
     n = 24
     page = np.array([160 * 1024, 48 * 1024 + 16, 4096, 32 * 1024, 112], np.int64)
-    for unroll in (0, 1, 2, 3, 4, 5, 6, 8, 10):
-        for wpc in (0, 3):
-            _lib.tune(_lib.TUNE_COPY_UNROLL, unroll)
-            _lib.tune(_lib.TUNE_COPY_WGS_PER_CU, wpc)
-            segs_np = [rng.integers(0, 256, (n, int(p)), dtype=np.uint8) for p in page[:4]]
-            perm = rng.permutation(n)
-            src, dst = perm[:9], perm[9:18]
-            segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
-            ops.copy_blocks(segs, src, dst)
-            oracle.copy_blocks([x.reshape(-1) for x in segs_np], page[:4], n, src, dst)
-            torch.cuda.synchronize()
-            for s in range(4):
-                assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (unroll, wpc, s)
+    for unroll, wpc, lds in itertools.product((0, 1, 2, 3, 4, 5, 6, 8, 10), (0, 3),
+                                              (0, 96 * 1024, 160 * 1024)):
+        _lib.tune(_lib.TUNE_COPY_UNROLL, unroll)
+        _lib.tune(_lib.TUNE_COPY_WGS_PER_CU, wpc)
+        _lib.tune(_lib.TUNE_COPY_LDS_BYTES, lds)
+        segs_np = [rng.integers(0, 256, (n, int(p)), dtype=np.uint8) for p in page[:4]]
+        perm = rng.permutation(n)
+        src, dst = perm[:9], perm[9:18]
+        segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+        ops.copy_blocks(segs, src, dst)
+        oracle.copy_blocks([x.reshape(-1) for x in segs_np], page[:4], n, src, dst)
+        torch.cuda.synchronize()
+        for s in range(4):
+            assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (unroll, wpc, lds, s)
 
 
 @pytest.mark.parametrize("shape_auto", [0, 1])

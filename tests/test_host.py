@@ -283,6 +283,9 @@ def test_tuning_knobs(aegkv_lib):
         _lib.tune(_lib.TUNE_AUTO_D2H, 7)
     with pytest.raises(ValueError):
         _lib.tune(99, 1)
+    assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_COPY_LDS_BYTES, 161 * 1024)
 
 
 def test_bench_refuses_more_than_one_gpu():
