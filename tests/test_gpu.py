@@ -399,6 +399,73 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     pool.free()
 
 
+# ------------------------------------------------------------- edge cases --
+
+@pytest.mark.parametrize("mode", MODES)
+def test_edge_cases_vs_oracle(gpu, oracle, restore_tuning, mode):
+    """Empty calls on every entry point; ids at both ends of each pool;
+    6-byte blocks (byte path) through the legacy swap; composite pages larger
+    than the staging chunk (one entry per chunk)."""
+    rng = np.random.default_rng(77)
+    # legacy swap, 6-byte blocks, ids 0 and N-1 on both sides
+    n_dev, n_host = 9, 5
+    cache_np = rng.integers(0, 256, (n_dev, 6), dtype=np.uint8)
+    pool_np = rng.integers(0, 256, (n_host, 6), dtype=np.uint8)
+    cache = torch.from_numpy(cache_np.copy()).view(torch.bfloat16).to(gpu)   # [9, 3] bf16
+    pool = torch.from_numpy(pool_np.copy()).view(torch.bfloat16).pin_memory()
+    ops.swap([], [], False, cache, pool, mode=mode)
+    ops.swap([], [], True, cache, pool, mode=mode)
+    ops.swap([0, n_dev - 1], [n_host - 1, 0], False, cache, pool, mode=mode)
+    oracle.swap_legacy([0, n_dev - 1], [n_host - 1, 0], False, cache_np, cache_np.size // 2,
+                       n_dev, pool_np)
+    ops.swap([n_host - 1, 0], [n_dev - 1, 0], True, cache, pool, mode=mode)
+    oracle.swap_legacy([n_host - 1, 0], [n_dev - 1, 0], True, cache_np, cache_np.size // 2,
+                       n_dev, pool_np)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.view(torch.uint8).numpy(), pool_np)
+    assert np.array_equal(cache.cpu().view(torch.uint8).numpy(), cache_np)
+
+    # composite page (1.5 MiB) above the 1 MiB staging chunk
+    _lib.tune(_lib.TUNE_STAGING_BYTES, 1 << 20)
+    page = np.array([512 * 1024, 1024 * 1024], np.int64)
+    cpu_off = np.array([0, 512 * 1024], np.int64)
+    owners = np.array([1, 1], np.uint64)
+    kpp = np.array([2], np.int64)
+    composite = int(page.sum())
+    n_gpu, n_hp = 6, 4
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    host_np = rng.integers(0, 256, (n_hp, composite), dtype=np.uint8)
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    hp = _pool_from(host_np)
+    lay = ops.SegmentLayout(segs, page, cpu_off, owners, n_gpu, kpp, hp.tensor, composite, 0)
+    e = np.zeros(0, np.int64)
+    lay.swap(e, e, e.astype(np.int32), e, e, False, mode=mode)
+    src, dst = np.array([0, n_gpu - 1, 2]), np.array([n_hp - 1, 0, 1])
+    grp, first, valid = np.zeros(3, np.int32), np.array([0, 1, 2]), np.array([2, 1, 0])
+    lay.swap(src, dst, grp, first, valid, False, mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       host_np.reshape(-1), composite, 0, composite, src, dst, grp, first,
+                       valid, False)
+    lay.swap(dst[::-1].copy(), src, grp, first, valid, True, mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       host_np.reshape(-1), composite, 0, composite, dst[::-1].copy(), src,
+                       grp, first, valid, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(hp.tensor.numpy().reshape(host_np.shape), host_np)
+    for s in range(2):
+        assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), s
+
+    # copy_blocks: empty, then the two ends of the pool
+    ops.copy_blocks(segs, [], [])
+    ops.copy_blocks(segs, [n_gpu - 1], [0])
+    oracle.copy_blocks([x.reshape(-1) for x in segs_np], page, n_gpu, [n_gpu - 1], [0])
+    torch.cuda.synchronize()
+    for s in range(2):
+        assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), s
+    del lay
+    hp.free()
+
+
 # --------------------------------------------------------- error behaviour --
 
 def test_rejections_enqueue_nothing(gpu):
