@@ -30,6 +30,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <deque>
 #include <map>
@@ -91,6 +92,41 @@ struct Tunables {
 Tunables g_tune;
 std::mutex g_tune_mu;
 constexpr int64_t kMaxLdsPerWorkgroup = int64_t(160) << 10;  // gfx950: 160 KiB per CU
+
+// Environment overrides, read once per process: AEGKV_AUTO_D2H and
+// AEGKV_AUTO_H2D ("direct" or "staged") choose what mode AUTO resolves to,
+// AEGKV_STAGING_BYTES (>= 1 MiB) the STAGED chunk. An invalid value makes
+// every entry point that moves data fail with AEGKV_EINVAL naming it.
+std::once_flag g_env_once;
+char g_env_err[256] = "";
+
+void read_env() {
+  std::lock_guard<std::mutex> lk(g_tune_mu);
+  auto mode = [](const char* name, int64_t* slot) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return;
+    if (!std::strcmp(v, "direct")) *slot = AEGKV_MODE_DIRECT;
+    else if (!std::strcmp(v, "staged")) *slot = AEGKV_MODE_STAGED;
+    else std::snprintf(g_env_err, sizeof(g_env_err), "%s=%s: expected direct or staged", name, v);
+  };
+  mode("AEGKV_AUTO_D2H", &g_tune.auto_d2h);
+  mode("AEGKV_AUTO_H2D", &g_tune.auto_h2d);
+  const char* v = std::getenv("AEGKV_STAGING_BYTES");
+  if (v && *v) {
+    char* end = nullptr;
+    const long long x = std::strtoll(v, &end, 10);
+    if (*end != '\0' || x < (1ll << 20))
+      std::snprintf(g_env_err, sizeof(g_env_err),
+                    "AEGKV_STAGING_BYTES=%s: expected an integer >= 1048576", v);
+    else
+      g_tune.staging_bytes = x;
+  }
+}
+
+int env_status() {
+  std::call_once(g_env_once, read_env);
+  return g_env_err[0] ? fail(AEGKV_EINVAL, "%s", g_env_err) : 0;
+}
 
 Tunables tunables() {
   std::lock_guard<std::mutex> lk(g_tune_mu);
@@ -925,6 +961,7 @@ int aegkv_abi_version(void) { return AEGKV_ABI_VERSION; }
 const char* aegkv_last_error(void) { return g_err; }
 
 int64_t aegkv_tune(int key, int64_t value) {
+  (void)env_status();  // environment overrides apply before the first change
   std::lock_guard<std::mutex> lk(g_tune_mu);
   int64_t* slot = nullptr;
   switch (key) {
@@ -972,6 +1009,7 @@ int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
                void* kv_swap, int64_t swap_num_blocks, int64_t block_bytes, int mode,
                hipStream_t stream) {
   g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
   if (block_bytes <= 0) return fail(AEGKV_EINVAL, "block_bytes must be positive");
   void* bases[1] = {kv_cache};
   const int64_t page[1] = {block_bytes};
@@ -995,6 +1033,7 @@ int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
                       const int64_t* valid_kernel_blocks, int is_swap_in, int mode,
                       hipStream_t stream) {
   g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
   if (num_entries > 0 && (!group_ids || !first_kernel_blocks || !valid_kernel_blocks))
     return fail(AEGKV_EINVAL, "entry metadata arrays must not be null");
   SwapLayout L{num_segments, segment_bases, segment_page_bytes, segment_host_offsets,
@@ -1011,6 +1050,7 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
                       int64_t num_pairs, const int64_t* src_block_ids,
                       const int64_t* dst_block_ids, hipStream_t stream) {
   g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
   if (num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
   if (!segment_bases || !segment_page_bytes)
     return fail(AEGKV_EINVAL, "segment arrays must not be null");

@@ -50,6 +50,12 @@ extern "C" {
 #define AEGKV_MODE_STAGED 2 /* gather/scatter kernel <-> contiguous device
                                staging, plus SDMA hipMemcpyAsync of merged runs */
 
+/* Environment, read once per process before the first call:
+ *   AEGKV_AUTO_D2H, AEGKV_AUTO_H2D = direct | staged   (what AUTO picks)
+ *   AEGKV_STAGING_BYTES = integer >= 1048576           (STAGED chunk)
+ * An invalid value makes aegkv_swap, aegkv_swap_blocks and
+ * aegkv_copy_blocks return AEGKV_EINVAL with a message naming it. */
+
 /* tuning keys for aegkv_tune (values < 0 query without changing) */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS 1 /* swap-out kernel: workgroups    */
 #define AEGKV_TUNE_STAGING_BYTES 2   /* max device staging per chunk      */

@@ -358,3 +358,30 @@ def test_copy_blocks_rejections_before_any_hip_call(aegkv_lib):
     assert call([1], [8]) == -2
     assert call([1], [2], blocks=1 << 62) == -2
     assert call([], []) == 0  # nothing to do, nothing touched
+
+
+def _run_with_env(env_extra, code):
+    import os
+    import sys
+
+    env = dict(os.environ, **env_extra)
+    res = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                         timeout=300, env=env, cwd=str(REPO))
+    assert res.returncode == 0, res.stderr
+    return res.stdout.strip()
+
+
+def test_environment_picks_auto_modes_and_staging(aegkv_lib):
+    code = ("from aegaeon_amd import _lib; "
+            "print(_lib.tune(_lib.TUNE_AUTO_D2H), _lib.tune(_lib.TUNE_AUTO_H2D), "
+            "_lib.tune(_lib.TUNE_STAGING_BYTES))")
+    out = _run_with_env({"AEGKV_AUTO_D2H": "staged", "AEGKV_STAGING_BYTES": str(64 << 20)}, code)
+    assert out.split() == ["2", "1", str(64 << 20)]
+
+
+def test_invalid_environment_fails_every_transfer_call(aegkv_lib):
+    code = ("from aegaeon_amd import _lib; lib = _lib.load(); "
+            "rc = lib.aegkv_copy_blocks(1, None, None, 1, 0, None, None, None); "
+            "print(rc, lib.aegkv_last_error().decode())")
+    out = _run_with_env({"AEGKV_AUTO_H2D": "fast"}, code)
+    assert out.startswith("-1 ") and "AEGKV_AUTO_H2D=fast" in out
