@@ -130,25 +130,14 @@ def swap(
     _lib.check(rc)
 
 
-class _OnDevice:
-    """Make `device` current for a call, switching only when it is not."""
-
-    __slots__ = ("index", "prev")
-
-    def __init__(self, device: torch.device):
-        self.index = device.index if device.index is not None else torch.cuda.current_device()
-        self.prev = None
-
-    def __enter__(self):
-        cur = torch.cuda.current_device()
-        if cur != self.index:
-            self.prev = cur
-            torch.cuda.set_device(self.index)
-
-    def __exit__(self, *exc):
-        if self.prev is not None:
-            torch.cuda.set_device(self.prev)
-            self.prev = None
+def _call_on(device: torch.device, fn):
+    """Run fn() with `device` current, switching (and restoring) only when
+    another device is current. Keeps no state, so threads may share it."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if torch.cuda.current_device() == index:
+        return fn()
+    with torch.cuda.device(index):
+        return fn()
 
 
 class SegmentLayout:
@@ -201,7 +190,6 @@ class SegmentLayout:
                       _pu64(self.owners), self.device_num_blocks, self.kpp.size,
                       _p64(self.kpp), host_pool.data_ptr(), self.host_num_blocks,
                       self.host_page_bytes, self.host_rank_offset)
-        self._on_device = _OnDevice(dev)
 
     def swap(self, source_block_ids, target_block_ids, group_ids, first_kernel_blocks,
              valid_kernel_blocks, is_swap_in: bool, *, mode="auto",
@@ -219,12 +207,10 @@ class SegmentLayout:
                 f"first={first.size}, valid={valid.size}"
             )
         lib = _lib.load()
-        with self._on_device:
-            rc = lib.aegkv_swap_blocks(
-                *self._args, src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
-                _p64(valid), 1 if is_swap_in else 0, _mode(mode),
-                _stream_ptr(self.device, stream),
-            )
+        rc = _call_on(self.device, lambda: lib.aegkv_swap_blocks(
+            *self._args, src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
+            _p64(valid), 1 if is_swap_in else 0, _mode(mode),
+            _stream_ptr(self.device, stream)))
         _lib.check(rc)
 
 
@@ -374,8 +360,7 @@ def fence_signal(words: torch.Tensor, index: int, value: int, *,
     if dev.type != "cuda":
         raise ValueError("fence words must live on the device")
     lib = _lib.load()
-    with _OnDevice(dev):
-        rc = lib.aegkv_fence_signal(ptr, int(value), _stream_ptr(dev, stream))
+    rc = _call_on(dev, lambda: lib.aegkv_fence_signal(ptr, int(value), _stream_ptr(dev, stream)))
     _lib.check(rc)
 
 
@@ -400,6 +385,6 @@ def fence_wait(words: torch.Tensor, index: int, value: int, timed_out: torch.Ten
         raise ValueError("fence words and the timed_out flags must live on one device")
     timeout_us = int(timeout_s * 1e6)
     lib = _lib.load()
-    with _OnDevice(dev):
-        rc = lib.aegkv_fence_wait(ptr, int(value), timeout_us, flag, _stream_ptr(dev, stream))
+    rc = _call_on(dev, lambda: lib.aegkv_fence_wait(ptr, int(value), timeout_us, flag,
+                                                    _stream_ptr(dev, stream)))
     _lib.check(rc)
