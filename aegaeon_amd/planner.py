@@ -53,7 +53,7 @@ class BlockPools:
         self.cpu_slab_size_bytes = cpu_slab_size_bytes
         self.cpu_free_blocks: Dict[Tuple[int, ...], Deque[int]] = defaultdict(deque)
         self.cpu_free_slabs: List[int] = list(range(cpu_num_slabs))
-        self.cpu_slab_usage: List[int] = [0] * cpu_num_slabs
+        self.cpu_slab_usage = np.zeros(cpu_num_slabs, np.int64)  # used blocks per slab
         self.cpu_block_shape: List[Optional[Tuple[int, ...]]] = [None] * cpu_num_slabs
         self.gpu_free_blocks: Dict[int, List[int]] = {}
         self.gpu_block_shape: Dict[int, Tuple[int, ...]] = {}
@@ -168,11 +168,14 @@ class BlockPools:
             lo, hi = slab_range(slab, self.cpu_slab_size_bytes, block_bytes)
             self.cpu_block_shape[slab] = block_shape
             free.extend(range(lo, hi))
-        out = []
-        for _ in range(num_blocks):
-            b = free.popleft()
-            self.cpu_slab_usage[b * block_bytes // self.cpu_slab_size_bytes] += 1
-            out.append(b)
+        # the first num_blocks ids of the deque, in order
+        out = list(itertools.islice(free, num_blocks))
+        rest = list(itertools.islice(free, num_blocks, None))
+        free.clear()
+        free.extend(rest)
+        if out:
+            slabs = np.asarray(out, np.int64) * block_bytes // self.cpu_slab_size_bytes
+            np.add.at(self.cpu_slab_usage, slabs, 1)
         return out
 
     def release(self, blocks: Sequence[int], location: int,
@@ -184,8 +187,9 @@ class BlockPools:
         block_shape = tuple(block_shape)
         block_bytes = self.block_size_bytes(block_shape)
         self.cpu_free_blocks[block_shape].extend(blocks)
-        for b in blocks:
-            self.cpu_slab_usage[b * block_bytes // self.cpu_slab_size_bytes] -= 1
+        if len(blocks):
+            slabs = np.asarray(blocks, np.int64) * block_bytes // self.cpu_slab_size_bytes
+            np.subtract.at(self.cpu_slab_usage, slabs, 1)
 
     def reclaim(self, plan: "SwapPlan") -> None:
         """Free a completed move's source ids (all of them, including pages
@@ -303,12 +307,14 @@ class MoveRecord:
 _KIND = {"attention": 0, "mamba_none": 1}
 
 
-def native_transfer_entries(groups: Sequence[CacheGroupConfig],
-                            tables: Sequence[Tuple[BlockTable, int]]
-                            ) -> List[List[Tuple[int, int, int, int, int]]]:
-    """BlockTable.transfer_entries for many tables sharing `groups`, in one
-    call into libaegkv (aegkv_transfer_entries). Returns one row list per
-    table, each row (group, column, block id, first, count)."""
+_Rows = Tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray, np.ndarray, np.ndarray]
+
+
+def _native_rows(groups: Sequence[CacheGroupConfig],
+                 tables: Sequence[Tuple[BlockTable, int]]) -> _Rows:
+    """aegkv_transfer_entries over many tables sharing `groups`: row arrays
+    (table index, group, column, block id, first, count), rows in table,
+    group, column order."""
     n_groups = len(groups)
     kind = np.array([_KIND[g.kind] for g in groups], np.int32)
     bs = np.array([g.block_size for g in groups], np.int64)
@@ -321,8 +327,9 @@ def native_transfer_entries(groups: Sequence[CacheGroupConfig],
         raise ValueError("every table must have one column list per cache group")
     offsets = np.zeros(len(lengths) + 1, np.int64)
     np.cumsum(lengths, out=offsets[1:])
-    ids = np.fromiter((b for table, _ in tables for col in table.group_blocks for b in col),
-                      dtype=np.int64, count=int(offsets[-1]))
+    ids = np.fromiter(itertools.chain.from_iterable(
+        col for table, _ in tables for col in table.group_blocks),
+        dtype=np.int64, count=int(offsets[-1]))
     cap = max(1, int(offsets[-1]))
     out = {name: np.empty(cap, np.int64) for name in ("table", "column", "block", "first",
                                                        "count")}
@@ -336,10 +343,27 @@ def native_transfer_entries(groups: Sequence[CacheGroupConfig],
         p64(out["block"]), p64(out["first"]), p64(out["count"]), ctypes.byref(n))
     _lib.check(rc)
     m = n.value
+    return (out["table"][:m], out_group[:m].astype(np.int64), out["column"][:m],
+            out["block"][:m], out["first"][:m], out["count"][:m])
+
+
+def _rows_from_lists(per_table: Sequence[Sequence[Tuple[int, int, int, int, int]]]) -> _Rows:
+    """Row arrays from BlockTable.transfer_entries lists, one per table."""
+    flat = [(t,) + row for t, rows in enumerate(per_table) for row in rows]
+    a = np.array(flat, np.int64).reshape(-1, 6)
+    return a[:, 0], a[:, 1], a[:, 2], a[:, 3], a[:, 4], a[:, 5]
+
+
+def native_transfer_entries(groups: Sequence[CacheGroupConfig],
+                            tables: Sequence[Tuple[BlockTable, int]]
+                            ) -> List[List[Tuple[int, int, int, int, int]]]:
+    """BlockTable.transfer_entries for many tables sharing `groups`, in one
+    call into libaegkv (aegkv_transfer_entries). Returns one row list per
+    table, each row (group, column, block id, first, count)."""
+    tbl, grp, col, blk, first, count = _native_rows(groups, tables)
     rows: List[List[Tuple[int, int, int, int, int]]] = [[] for _ in tables]
-    cols = zip(out["table"][:m].tolist(), out_group[:m].tolist(), out["column"][:m].tolist(),
-               out["block"][:m].tolist(), out["first"][:m].tolist(), out["count"][:m].tolist())
-    for t, g, c, b, f, k in cols:
+    for t, g, c, b, f, k in zip(tbl.tolist(), grp.tolist(), col.tolist(), blk.tolist(),
+                                first.tolist(), count.tolist()):
         rows[t].append((g, c, b, f, k))
     return rows
 
@@ -419,32 +443,33 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
     # every moved table shares the source's cache groups; plan them in one call
     groups = plans[0][0].cache_groups
     if all(tuple(t.cache_groups) == tuple(groups) for t, _, _ in plans):
-        native = native_transfer_entries(groups, [(t, tok) for t, tok, _ in plans])
-        plans = [(t, tok, rows) for (t, tok, _), rows in zip(plans, native)]
+        rows = _native_rows(groups, [(t, tok) for t, tok, _ in plans])
     else:
-        plans = [(t, tok, t.transfer_entries(tok)) for t, tok, _ in plans]
-    targets = pools.allocate(sum(len(e) for _, _, e in plans), target_location, shape)
+        rows = _rows_from_lists([t.transfer_entries(tok) for t, tok, _ in plans])
+    tbl, grp, col, blk, first, count = rows
+    targets = np.asarray(pools.allocate(int(tbl.size), target_location, shape), np.int64)
+    # copy lists: retained pages with live bytes, in table, group, column order
+    live = count > 0
     plan = SwapPlan(moved_ids, src_loc, target_location, shape,
+                    source_block_ids=blk[live].tolist(),
+                    target_block_ids=targets[live].tolist(),
+                    group_ids=grp[live].tolist(),
+                    first_kernel_blocks=first[live].tolist(),
+                    valid_kernel_blocks=count[live].tolist(),
                     release_source_block_ids=release)
-    cursor = 0
-    new_tables = []
-    for table, tokens, entries in plans:
-        mine = targets[cursor:cursor + len(entries)]
-        cursor += len(entries)
-        # destination table: retained columns get their new ids, everything
-        # else stays released (BlockTable.moved_group_blocks, same rows)
-        moved = [[-1] * len(col) for col in table.group_blocks]
-        for (g, col, pid, first, count), tid in zip(entries, mine):
-            moved[g][col] = tid
-            if count > 0:
-                plan.source_block_ids.append(pid)
-                plan.target_block_ids.append(tid)
-                plan.group_ids.append(g)
-                plan.first_kernel_blocks.append(first)
-                plan.valid_kernel_blocks.append(count)
-        new_tables.append(moved)
-    for (table, _, _), groups in zip(plans, new_tables):
-        table.group_blocks = groups
+    # destination tables: retained columns get their new ids, everything
+    # else stays released (BlockTable.moved_group_blocks, same rows)
+    bounds = np.searchsorted(tbl, np.arange(len(plans) + 1))
+    for i, (table, _, _) in enumerate(plans):
+        lo, hi = int(bounds[i]), int(bounds[i + 1])
+        g_i, c_i, t_i = grp[lo:hi], col[lo:hi], targets[lo:hi]
+        moved = []
+        for g, cols in enumerate(table.group_blocks):
+            new = np.full(len(cols), -1, np.int64)
+            sel = g_i == g
+            new[c_i[sel]] = t_i[sel]
+            moved.append(new.tolist())
+        table.group_blocks = moved
         table.location = target_location
     return plan
 

@@ -11,7 +11,8 @@ One step = one pass of the path over one batch:
   * Llama-2-13B KV shape (80 x [8192,16,40,128] fp16): copy_blocks of 4096
     (src, dst) pairs, distinct targets disjoint from the sources.
 Every operation is one libaegkv call on the current stream, timed with HIP
-events recorded on that stream. `value` is the swap throughput (both
+events recorded on that stream. Other configs (--config): varlen, overlap,
+refplan, switch (see --help). `value` is the swap throughput (both
 directions' bytes over their summed time); the copy_blocks kernel carries
 the HBM roofline, the swaps the measured-host-link roofline.
 
@@ -55,12 +56,14 @@ def parse():
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
     p.add_argument("--config", default="headline",
-                   choices=["headline", "varlen", "overlap", "refplan"],
+                   choices=["headline", "varlen", "overlap", "refplan", "switch"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
                         "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
                         "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams; "
                         "refplan: the reference benchmark's extent plans, libaegkv beside "
-                        "the reference's per-extent copy_ loop on the same GPU")
+                        "the reference's per-extent copy_ loop on the same GPU; switch: "
+                        "two models' KV swapped out and in at once through the planner, "
+                        "swapper and move ledger")
     return p.parse_args()
 
 
@@ -402,6 +405,135 @@ def bench_overlap(args):
     }
 
 
+def bench_switch(args):
+    """Token-level model switch through the whole host stack: two engines
+    (models A and B, Qwen2.5-7B KV shape 56 x [16384,16,4,128] bf16 each) on
+    one GPU and one pinned host pool. A switch moves every request of the
+    active model out (plan_move -> KVSwapper.swap_blocks on its swap-out
+    stream -> BlockPools.record_move) and every request of the other model in
+    (same, swap-in stream, waiting on the requests' previous move events), so
+    both link directions run at once. 64 requests per model, log-normal
+    lengths as in the variable-length config; device free lists start
+    shuffled so ids are scattered."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+    from aegaeon_amd.cache_groups import BlockTable, CacheGroupConfig, CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import allocate_composite_cache, kv_tensor_specs
+    from aegaeon_amd.planner import BLOCK_LOCATION_CPU, BlockPools, plan_move
+    from aegaeon_amd.swapper import KVSwapper
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    bidir = measure_link_bidir(torch, ops, dev)   # before the swappers create their streams
+    L, NB, H, D, NREQ = 28, 16384, 4, 128, 64
+    specs = kv_tensor_specs(L, NB, 16, H, D, 2)
+    names = [{f"layers.{l}.{kv}" for l in range(L) for kv in ("k", "v")}]
+    groups = (CacheGroupConfig("attention", 16, 16),)
+    descr = [CacheGroupRuntimeConfig("attention", 16, 16)]
+    caches = [allocate_composite_cache(specs, NB, dev) for _ in range(2)]
+    g = torch.Generator(device=dev).manual_seed(5)
+    for c in caches:
+        for t in c.backing:
+            t.view(torch.int32).random_(generator=g)
+    page = caches[0].page_size_bytes
+    shape = (page // 2,)
+    rng = np.random.default_rng(5)
+    lengths = [np.clip(np.round(np.exp(rng.normal(np.log(1024.0), 1.0, NREQ))), 16, 32768)
+               .astype(np.int64) for _ in range(2)]
+    blocks = [int(np.ceil(x / 16).sum()) for x in lengths]
+    slab = 1 << 30
+    n_slabs = -(-sum(blocks) * page // slab) + 4
+    pools = BlockPools(n_slabs, slab)
+    host = ops.PinnedHostPool(n_slabs * slab)
+    sw = []
+    for e in range(2):
+        pools.register_gpu_space(e, NB, shape, groups)
+        free = pools.gpu_free_blocks[e]
+        free[:] = list(rng.permutation(free))
+        sw.append(KVSwapper(caches[e], names, descr, host.tensor))
+    tables, reqs = {}, [[], []]
+    for e in range(2):
+        for i, tok in enumerate(lengths[e]):
+            rid = e * 1000 + i
+            n = groups[0].table_blocks_for_tokens(int(tok))
+            tables[rid] = BlockTable(e, shape, groups, [pools.allocate(n, e, shape)])
+            reqs[e].append((rid, int(tok)))
+    # reference copies of every request's blocks, to check the final state
+    want = {}
+    for e in range(2):
+        for rid, _ in reqs[e]:
+            ids = torch.tensor(tables[rid].group_blocks[0], device=dev)
+            want[rid] = [t.view(torch.uint8).view(NB, -1)[ids].clone() for t in caches[e].backing]
+    latest = {}
+
+    def move(e, target):
+        plan = plan_move(reqs[e], tables, target, pools)
+        s = sw[e]
+        ev = s.swap_blocks(plan.request_ids, plan.source_block_ids, plan.target_block_ids,
+                           plan.group_ids, plan.first_kernel_blocks, plan.valid_kernel_blocks,
+                           [latest.get(r) for r in plan.request_ids], plan.is_swap_in)
+        pools.record_move(plan, [ev])
+        for r in plan.request_ids:
+            latest[r] = ev
+        return ev, len(plan.source_block_ids) * page
+
+    log("parking model B on the host")
+    move(1, BLOCK_LOCATION_CPU)[0].synchronize()
+    active = 0
+    runs = []
+    for it in range(args.warmup + args.steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ev_out, b_out = move(active, BLOCK_LOCATION_CPU)
+        ev_in, b_in = move(1 - active, 1 - active)
+        t1 = time.perf_counter()
+        ev_out.synchronize()
+        ev_in.synchronize()
+        t2 = time.perf_counter()
+        pools.reclaim_gpu_moves(active, wait=False)
+        pools.reclaim_cpu_moves(shape, wait=False)
+        if it >= args.warmup:
+            runs.append((t2 - t0, t1 - t0, b_out, b_in))
+        active = 1 - active
+    # bring everything back to its own engine and compare with the copies
+    for e in range(2):
+        if tables[reqs[e][0][0]].location != e:
+            move(e, e)[0].synchronize()
+    ok = True
+    for e in range(2):
+        for rid, _ in reqs[e]:
+            ids = torch.tensor(tables[rid].group_blocks[0], device=dev)
+            got = [t.view(torch.uint8).view(NB, -1)[ids] for t in caches[e].backing]
+            ok = ok and all(torch.equal(a, b) for a, b in zip(got, want[rid]))
+    if not ok:
+        raise AssertionError("model-switch round trips are not bit-exact")
+    wall = statistics.median(r[0] for r in runs)
+    host_ms = statistics.median(r[1] for r in runs) * 1e3
+    moved = statistics.median(r[2] + r[3] for r in runs)
+    host.free()
+    return {
+        "metric": "model-switch wall time and link rate through planner + swapper + ledger",
+        "unit": "GB/s",
+        "config": {"workload": "two Qwen2.5-7B KV caches (56 x [16384,16,4,128] bf16 each), "
+                               f"{NREQ} requests per model, log-normal lengths (median 1024, "
+                               "sigma 1.0); each switch swaps the active model out and the other "
+                               "in at once",
+                   "blocks": {"A": blocks[0], "B": blocks[1]}, "page_bytes": page,
+                   "switches": args.steps, "warmup": args.warmup},
+        "switch_wall_ms": round(wall * 1e3, 3),
+        "host_plan_and_enqueue_ms": round(host_ms, 3),
+        "bytes_per_switch": int(moved),
+        "link_aggregate_GBps": round(moved / wall / 1e9, 3),
+        "link_bidirectional_ceiling_GBps": round(bidir, 3),
+        "frac_bidirectional_ceiling": round(moved / wall / 1e9 / bidir, 4),
+        "statistic": "median over switches",
+        "bit_exact": True,
+    }
+
+
 def reference_submit_copies(cpu_pages, gpu_segments, extents, is_swap_in):
     """The reference benchmark's copy loop (benchmark_composite_swap.py:67-87):
     one narrow().copy_(non_blocking=True) per (segment, page) extent."""
@@ -590,7 +722,7 @@ def main():
         sys.exit(2)
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap,
-              "refplan": bench_refplan}[args.config]
+              "refplan": bench_refplan, "switch": bench_switch}[args.config]
         print(json.dumps(fn(args)), flush=True)
         return
     import numpy as np
