@@ -42,6 +42,7 @@ TUNE_SWAP_SHAPE_AUTO = 8
 TUNE_SWAP_IN_WORKGROUPS = 9
 TUNE_STAGED_DMA_STREAMS = 10
 TUNE_COPY_LDS_BYTES = 11
+TUNE_SWAP_UNROLL = 12
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (

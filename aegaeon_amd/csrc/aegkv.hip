@@ -83,6 +83,7 @@ struct Tunables {
   int64_t copy_wgs_per_cu = 0;   // copy_blocks: 0 = one workgroup per work item
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
+  int64_t swap_unroll = 4;       // swap kernels: 16 B loads per lane (256-lane shape)
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
@@ -770,7 +771,8 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   char* dv = ctx->ring.dev + off;
   const Tunables t = tunables();
   const ShapeSel sh = !vec ? ShapeSel{256, 1}
-                           : (t.swap_shape_auto ? auto_shape(max_page) : ShapeSel{256, 4});
+                           : (t.swap_shape_auto ? auto_shape(max_page)
+                                                : ShapeSel{256, static_cast<int>(t.swap_unroll)});
   const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
   const int64_t items = n * S * cpt;
   if (items >= (int64_t(1) << 32)) {
@@ -974,6 +976,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_COPY_WGS_PER_CU: slot = &g_tune.copy_wgs_per_cu; break;
     case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
     case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
+    case AEGKV_TUNE_SWAP_UNROLL: slot = &g_tune.swap_unroll; break;
     case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
     case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
@@ -990,6 +993,8 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "staging must be at least 1 MiB");
     if (key == AEGKV_TUNE_COPY_WGS_PER_CU && value > 64)
       return fail(AEGKV_EINVAL, "copy workgroups per CU must be in [0, 64]");
+    if (key == AEGKV_TUNE_SWAP_UNROLL && value != 1 && value != 2 && value != 4)
+      return fail(AEGKV_EINVAL, "swap unroll must be 1, 2 or 4");
     if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && !valid_copy_unroll(value))
       return fail(AEGKV_EINVAL, "copy unroll must be 0 (auto) or one of 1,2,3,4,5,6,8,10");
     if (key == AEGKV_TUNE_STAGED_DMA_STREAMS && value > kMaxDmaStreams)

@@ -76,6 +76,8 @@ extern "C" {
                                         >= 32 KiB items: LDS bytes reserved
                                         per workgroup (0 - 160 KiB; caps
                                         workgroups per CU; default 96 KiB) */
+#define AEGKV_TUNE_SWAP_UNROLL 12    /* swap kernels: 16 B loads per lane of
+                                        the 256-lane shape (1, 2 or 4)      */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

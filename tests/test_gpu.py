@@ -283,7 +283,8 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
 def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
-            _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES)
+            _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
+            _lib.TUNE_SWAP_UNROLL)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -313,10 +314,11 @@ def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
             assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (unroll, wpc, lds, s)
 
 
-@pytest.mark.parametrize("shape_auto", [0, 1])
+@pytest.mark.parametrize("shape_auto,unroll", [(0, 4), (0, 2), (0, 1), (1, 4)])
 @pytest.mark.parametrize("wpc", [1, 37, 4096])
-def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, wpc):
+def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, unroll, wpc):
     _lib.tune(_lib.TUNE_SWAP_SHAPE_AUTO, shape_auto)
+    _lib.tune(_lib.TUNE_SWAP_UNROLL, unroll)
     _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS, wpc)
     _lib.tune(_lib.TUNE_SWAP_IN_WORKGROUPS, wpc)
     rng = np.random.default_rng(31 + wpc)

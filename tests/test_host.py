@@ -284,6 +284,9 @@ def test_tuning_knobs(aegkv_lib):
     with pytest.raises(ValueError):
         _lib.tune(99, 1)
     assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
+    assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 4
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_SWAP_UNROLL, 3)
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_COPY_LDS_BYTES, 161 * 1024)
 
