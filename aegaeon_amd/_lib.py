@@ -43,6 +43,7 @@ TUNE_SWAP_IN_WORKGROUPS = 9
 TUNE_STAGED_DMA_STREAMS = 10
 TUNE_COPY_LDS_BYTES = 11
 TUNE_SWAP_UNROLL = 12
+HOST_UNCACHED = 1
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (
@@ -54,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_copy_blocks",
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
+    "aegkv_host_alloc_flags",
     "aegkv_host_free",
     "aegkv_fence_signal",
     "aegkv_fence_wait",
@@ -85,6 +87,7 @@ _SIGNATURES = {
          _I64P, _I64P, _I64P, _I64P, _I64P],
     ),
     "aegkv_host_alloc": (_INT, [_PP, _I64]),
+    "aegkv_host_alloc_flags": (_INT, [_PP, _I64, _INT]),
     "aegkv_host_free": (_INT, [_P]),
     "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
     "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),

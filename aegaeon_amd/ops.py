@@ -314,15 +314,22 @@ class PinnedHostPool:
     gone (views keep it alive), so a kernel can never be handed freed
     memory through a surviving view. Callers still wait for GPU work on the
     pool before dropping the last view.
+
+    uncached=True allocates from the uncached system pool
+    (AEGKV_HOST_UNCACHED): faster swaps, especially both directions at
+    once, but the library keeps such memory mapped until the process ends
+    and reuses it for later uncached pools of a fitting size.
     """
 
-    def __init__(self, nbytes: int):
+    def __init__(self, nbytes: int, uncached: bool = False):
         if nbytes <= 0:
             raise ValueError("pool size must be positive")
         lib = _lib.load()
         ptr = ctypes.c_void_p()
-        _lib.check(lib.aegkv_host_alloc(ctypes.byref(ptr), int(nbytes)))
+        _lib.check(lib.aegkv_host_alloc_flags(ctypes.byref(ptr), int(nbytes),
+                                              _lib.HOST_UNCACHED if uncached else 0))
         self.nbytes = int(nbytes)
+        self.uncached = uncached
         buf = (ctypes.c_uint8 * self.nbytes).from_address(ptr.value)
         fin = weakref.finalize(buf, _free_pinned, ptr.value)
         fin.atexit = False  # at interpreter exit the process releases it

@@ -246,7 +246,7 @@ def bench_varlen(args):
     n_slabs = -(-total * page // slab) + 2
     pools = BlockPools(n_slabs, slab)
     host_ids = np.array(pools.allocate(total, BLOCK_LOCATION_CPU, (page // 2,)), np.int64)
-    pool = ops.PinnedHostPool(n_slabs * slab)
+    pool = ops.PinnedHostPool(n_slabs * slab, uncached=True)
     common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
     lay = ops.SegmentLayout(segs, *common)
     z = np.zeros(total, np.int32)
@@ -316,11 +316,11 @@ def bench_overlap(args):
     # memory lower run the same shape with 3/4 of the swapped blocks.
     scale = 1.0
     try:
-        pool = ops.PinnedHostPool((NOUT + NIN) * page)
+        pool = ops.PinnedHostPool((NOUT + NIN) * page, uncached=True)
     except _lib.AegkvError:
         scale = 0.75
         NOUT, NIN = int(NOUT * scale), int(NIN * scale)
-        pool = ops.PinnedHostPool((NOUT + NIN) * page)
+        pool = ops.PinnedHostPool((NOUT + NIN) * page, uncached=True)
         log(f"pinned pool capped: running swap-out {NOUT}, swap-in {NIN} blocks")
     rng = np.random.default_rng(4)
     perm = rng.permutation(NB)
@@ -447,7 +447,7 @@ def bench_switch(args):
     slab = 1 << 30
     n_slabs = -(-sum(blocks) * page // slab) + 4
     pools = BlockPools(n_slabs, slab)
-    host = ops.PinnedHostPool(n_slabs * slab)
+    host = ops.PinnedHostPool(n_slabs * slab, uncached=True)
     sw = []
     for e in range(2):
         pools.register_gpu_space(e, NB, shape, groups)
@@ -610,7 +610,7 @@ def bench_refplan(args):
                  "optimized": [(0, kpp)] * fixed + [
                      kernel_block_extent_for_attention_page(length, b, phys_tok, kern_tok)
                      for b in range(pages - fixed)]}
-        host = ops.PinnedHostPool(pages * phys_bytes)
+        host = ops.PinnedHostPool(pages * phys_bytes, uncached=True)
         segs = [torch.empty(pages, seg_page, dtype=torch.uint8, device=dev) for _ in range(seg_n)]
         for t in segs:
             t.random_(0, 256)
@@ -649,7 +649,7 @@ def bench_refplan(args):
     S1, NB1, tile1, HOST1, n = 72, 8192, 32768, 4096, 1024
     segs1 = kv_segments(torch, 36, NB1, 8, 128, torch.bfloat16, dev, 1)
     pages1 = [t.view(torch.uint8).view(NB1, tile1) for t in segs1]
-    pool = ops.PinnedHostPool(HOST1 * S1 * tile1)
+    pool = ops.PinnedHostPool(HOST1 * S1 * tile1, uncached=True)
     hv = pool.tensor.view(HOST1, S1 * tile1)
     g = torch.Generator().manual_seed(1)
     out_ids = (torch.randperm(NB1 - 1, generator=g)[:n] + 1).numpy()
@@ -744,7 +744,7 @@ def main():
     segs1 = kv_segments(torch, L1, NB1, H1, D1, torch.bfloat16, dev, 1)
     S1 = len(segs1)
     tile1 = 16 * H1 * D1 * 2
-    pool = ops.PinnedHostPool(HOST1 * S1 * tile1)
+    pool = ops.PinnedHostPool(HOST1 * S1 * tile1, uncached=True)
     g = torch.Generator().manual_seed(1)
     out_ids = (torch.randperm(NB1 - 1, generator=g)[:NSW] + 1).numpy()
     host_ids = torch.randperm(HOST1, generator=g)[:NSW].numpy()
@@ -840,6 +840,7 @@ def main():
             "swap_bytes_per_direction": swap_bytes,
             "copy_blocks_bytes_rw": copy_bytes,
             "transfer_mode": {"d2h": mode_d2h, "h2d": mode_h2d},
+            "host_pool": "pinned, uncached (aegkv_host_alloc_flags AEGKV_HOST_UNCACHED)",
         },
         "swap": {
             "d2h_GBps": round(d2h_gbps, 3),

@@ -197,6 +197,20 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
  * device may access it). The pool is not zero-filled.
  */
 int aegkv_host_alloc(void** ptr, int64_t bytes);
+
+/*
+ * As aegkv_host_alloc, with flags. AEGKV_HOST_UNCACHED allocates the pool
+ * from the uncached (MTYPE UC) fine-grained system pool
+ * (hipHostMallocUncached): kernel loads and stores to it bypass the GPU L2.
+ * Measured on MI355X with the swap kernels: swap-out 56.6 -> 57.0 GB/s,
+ * both directions at once 87 -> 90 GB/s; a blit hipMemcpyAsync is
+ * unchanged. Such a pool is never returned to the runtime before the
+ * process ends: aegkv_host_free parks it, and a later uncached allocation
+ * whose size it fits (wasting at most a quarter) reuses it. Meant for
+ * long-lived pools such as a KV host pool.
+ */
+#define AEGKV_HOST_UNCACHED 1
+int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags);
 int aegkv_host_free(void* ptr);
 
 /*

@@ -401,6 +401,48 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     pool.free()
 
 
+# ------------------------------------------------------- uncached host pool --
+
+@pytest.mark.parametrize("mode", MODES)
+def test_uncached_host_pool_vs_oracle(gpu, oracle, mode):
+    """Swaps through an uncached (MTYPE UC) pool land where the oracle puts
+    them; a released uncached pool is parked and reused by the next
+    uncached pool of a fitting size."""
+    rng = np.random.default_rng(90)
+    kpp, page, owners, cpu_off = _random_layout(rng)
+    composite = int(page.sum())
+    n_gpu, n_host, n = 24, 20, 16
+    segs_np = [rng.integers(0, 256, (n_gpu, int(p)), dtype=np.uint8) for p in page]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    first_pool = ops.PinnedHostPool(n_host * composite, uncached=True)
+    first_ptr = first_pool.tensor.data_ptr()
+    first_pool.free()
+    pool = ops.PinnedHostPool(n_host * composite, uncached=True)
+    assert pool.tensor.data_ptr() == first_ptr          # parked memory reused
+    host_np = rng.integers(0, 256, (n_host, composite), dtype=np.uint8)
+    pool.tensor.copy_(torch.from_numpy(host_np.reshape(-1)))
+    grp = rng.integers(0, 3, n).astype(np.int32)
+    first = np.array([rng.integers(0, kpp[g] + 1) for g in grp], np.int64)
+    valid = np.array([rng.integers(0, kpp[g] - f + 1) for g, f in zip(grp, first)], np.int64)
+    lay = ops.SegmentLayout(segs, page, cpu_off, owners, n_gpu, kpp, pool.tensor, composite, 0)
+    src, dst = rng.permutation(n_gpu)[:n], rng.permutation(n_host)[:n]
+    lay.swap(src, dst, grp, first, valid, False, mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       host_np.reshape(-1), composite, 0, composite, src, dst, grp, first,
+                       valid, False)
+    back = rng.permutation(n_gpu)[:n]
+    lay.swap(dst, back, grp, first, valid, True, mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, cpu_off, owners, n_gpu, kpp,
+                       host_np.reshape(-1), composite, 0, composite, dst, back, grp, first,
+                       valid, True)
+    torch.cuda.synchronize()
+    assert np.array_equal(pool.tensor.numpy().reshape(host_np.shape), host_np)
+    for s in range(len(page)):
+        assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), s
+    del lay
+    pool.free()
+
+
 # ------------------------------------------------------------- edge cases --
 
 @pytest.mark.parametrize("mode", MODES)

@@ -388,3 +388,15 @@ def test_invalid_environment_fails_every_transfer_call(aegkv_lib):
             "print(rc, lib.aegkv_last_error().decode())")
     out = _run_with_env({"AEGKV_AUTO_H2D": "fast"}, code)
     assert out.startswith("-1 ") and "AEGKV_AUTO_H2D=fast" in out
+
+
+def test_host_alloc_flags_rejections(aegkv_lib):
+    import ctypes
+
+    from aegaeon_amd import _lib
+
+    p = ctypes.c_void_p()
+    assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 4096, 2) == _lib.EINVAL
+    assert b"flags" in aegkv_lib.aegkv_last_error()
+    assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 0, 1) == _lib.EINVAL
+    assert aegkv_lib.aegkv_host_alloc_flags(None, 16, 1) == _lib.EINVAL
