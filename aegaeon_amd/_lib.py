@@ -53,6 +53,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_swap",
     "aegkv_swap_blocks",
     "aegkv_copy_blocks",
+    "aegkv_migrate_blocks",
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
     "aegkv_host_alloc_flags",
@@ -81,6 +82,7 @@ _SIGNATURES = {
          _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P],
     ),
     "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_transfer_entries": (
         _INT,
         [_I32, _I32P, _I64P, _I64P, _I64P, _I64, _I64P, _I64P, _I64P, _I64, _I64P, _I32P,

@@ -159,6 +159,14 @@ struct PairDesc {
   int64_t dst;
 };
 
+struct CopySeg {            // one backing tensor of a block copy
+  const char* src;          // source cache's tensor
+  char* dst;                // target cache's tensor (== src within one cache)
+  int64_t page_bytes;
+  int64_t pad;
+};
+static_assert(sizeof(CopySeg) == 32, "CopySeg layout");
+
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) v4u gv4u;  // global (VM) address space
 typedef __attribute__((address_space(1))) char gchar;
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(WG) void swap_tiles_kernel(
 // copy_blocks: item w -> (pair p, segment s, chunk c), pair-major.
 template <int WG, int U, bool VEC, bool NT_STORE>
 __global__ __launch_bounds__(WG) void copy_blocks_kernel(
-    const SegDesc* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
+    const CopySeg* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
     uint32_t num_items, uint32_t chunks_per_tile) {
   constexpr int64_t kChunk = Shape<WG, U>::kChunk;
   for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
@@ -266,13 +274,13 @@ __global__ __launch_bounds__(WG) void copy_blocks_kernel(
     const uint32_t p = tile / num_segs;
     const uint32_t s = tile - p * num_segs;
     const PairDesc pr = pairs[p];
-    const SegDesc seg = segs[s];
+    const CopySeg seg = segs[s];
     const int64_t begin = static_cast<int64_t>(c) * kChunk;
     if (begin >= seg.page_bytes) continue;
     const uint32_t nbytes = static_cast<uint32_t>(
         (seg.page_bytes - begin < kChunk) ? (seg.page_bytes - begin) : kChunk);
-    const char* src = seg.base + pr.src * seg.page_bytes + begin;
-    char* dst = seg.base + pr.dst * seg.page_bytes + begin;
+    const char* src = seg.src + pr.src * seg.page_bytes + begin;
+    char* dst = seg.dst + pr.dst * seg.page_bytes + begin;
     if (VEC)
       move_chunk16<WG, U, NT_STORE>(src, dst, nbytes);
     else
@@ -562,7 +570,7 @@ hipError_t launch_swap(ShapeSel sh, bool to_host, bool vec, bool nt, int64_t gri
 // `lds`: dynamic LDS reserved per workgroup. The kernel does not use it; it
 // caps how many workgroups share a CU.
 template <int WG, int U, bool VEC, bool NT>
-hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const SegDesc* s,
+hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const CopySeg* s,
                          const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
   hipLaunchKernelGGL((copy_blocks_kernel<WG, U, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
                      dim3(WG), lds, st, s, p, ns, items, cpt);
@@ -570,7 +578,7 @@ hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const SegDe
 }
 
 hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, unsigned lds,
-                       hipStream_t st, const SegDesc* s, const PairDesc* p, uint32_t ns,
+                       hipStream_t st, const CopySeg* s, const PairDesc* p, uint32_t ns,
                        uint32_t items, uint32_t cpt) {
   if (!vec) return launch_copy_t<256, 1, false, false>(grid, 0, st, s, p, ns, items, cpt);
 #define AEGKV_CP(W, UU)                                                               \
@@ -960,6 +968,118 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   return 0;
 }
 
+// Whole-block copies from a source cache to a target cache (the same cache
+// for copy_blocks). Validates everything before touching the GPU.
+int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
+              const int64_t* page_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
+              int64_t num_pairs, const int64_t* src_ids, const int64_t* dst_ids, bool same_cache,
+              hipStream_t stream) {
+  if (num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
+  if (!src_bases || !dst_bases || !page_bytes)
+    return fail(AEGKV_EINVAL, "segment arrays must not be null");
+  if (src_num_blocks <= 0 || dst_num_blocks <= 0)
+    return fail(AEGKV_EINVAL, "device_num_blocks must be positive");
+  if (num_pairs < 0) return fail(AEGKV_EINVAL, "num_pairs must be >= 0");
+  if (num_pairs > 0 && (!src_ids || !dst_ids))
+    return fail(AEGKV_EINVAL, "block id arrays must not be null");
+  bool vec = true;
+  int64_t max_page = 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    if (!src_bases[s] || !dst_bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
+    if (page_bytes[s] <= 0)
+      return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
+    if (!mul_fits(src_num_blocks, page_bytes[s]) || !mul_fits(dst_num_blocks, page_bytes[s]))
+      return fail(AEGKV_ERANGE, "segment %d of %lld x %lld bytes overflows", s,
+                  static_cast<long long>(std::max(src_num_blocks, dst_num_blocks)),
+                  static_cast<long long>(page_bytes[s]));
+    if (!same_cache) {
+      const uintptr_t a0 = reinterpret_cast<uintptr_t>(src_bases[s]);
+      const uintptr_t b0 = reinterpret_cast<uintptr_t>(dst_bases[s]);
+      const uintptr_t a1 = a0 + static_cast<uint64_t>(src_num_blocks * page_bytes[s]);
+      const uintptr_t b1 = b0 + static_cast<uint64_t>(dst_num_blocks * page_bytes[s]);
+      if (a0 < b1 && b0 < a1)
+        return fail(AEGKV_EOVERLAP,
+                    "segment %d: source and target caches overlap (copy within one cache "
+                    "with aegkv_copy_blocks)", s);
+    }
+    vec = vec && aligned16(src_bases[s]) && aligned16(dst_bases[s]) && page_bytes[s] % 16 == 0;
+    max_page = std::max(max_page, page_bytes[s]);
+  }
+  // target roles: 0 = untouched, 1 = source, 2 = target (sources only matter in one cache)
+  std::vector<uint8_t> role(static_cast<size_t>(dst_num_blocks), 0);
+  for (int64_t i = 0; i < num_pairs; ++i) {
+    const int64_t s = src_ids[i], d = dst_ids[i];
+    if (s < 0 || s >= src_num_blocks || d < 0 || d >= dst_num_blocks)
+      return fail(AEGKV_ERANGE, "pair %lld (%lld -> %lld) outside [0, %lld) -> [0, %lld)",
+                  static_cast<long long>(i), static_cast<long long>(s),
+                  static_cast<long long>(d), static_cast<long long>(src_num_blocks),
+                  static_cast<long long>(dst_num_blocks));
+    if (role[static_cast<size_t>(d)] == 2)
+      return fail(AEGKV_EDUP, "target block id %lld appears twice", static_cast<long long>(d));
+    if (role[static_cast<size_t>(d)] == 1)
+      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
+                  static_cast<long long>(d));
+    role[static_cast<size_t>(d)] = 2;
+  }
+  if (same_cache) {
+    for (int64_t i = 0; i < num_pairs; ++i) {
+      const int64_t s = src_ids[i];
+      if (role[static_cast<size_t>(s)] == 2)
+        return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
+                    static_cast<long long>(s));
+      role[static_cast<size_t>(s)] = 1;
+    }
+  }
+  if (num_pairs == 0) return 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    int rc = check_device_range(src_bases[s], src_num_blocks * page_bytes[s], "segment base");
+    if (rc) return rc;
+    if (!same_cache) {
+      rc = check_device_range(dst_bases[s], dst_num_blocks * page_bytes[s], "target segment base");
+      if (rc) return rc;
+    }
+  }
+  const Tunables t = tunables();
+  ShapeSel sh = auto_shape(max_page);
+  if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};
+  if (!vec) sh = ShapeSel{256, 1};
+  const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
+  const int64_t items = num_pairs * num_segments * cpt;
+  if (items >= (int64_t(1) << 32))
+    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
+                static_cast<long long>(items));
+  DeviceCtx* ctx = nullptr;
+  int rc = get_ctx(&ctx);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const size_t seg_bytes = sizeof(CopySeg) * num_segments;
+  const size_t pair_off = (seg_bytes + 255) & ~size_t(255);
+  const size_t total = pair_off + sizeof(PairDesc) * num_pairs;
+  size_t off = 0;
+  rc = ring_reserve(ctx->ring, total, &off);
+  if (rc) return rc;
+  char* h = ctx->ring.host + off;
+  CopySeg* hs = reinterpret_cast<CopySeg*>(h);
+  for (int32_t s = 0; s < num_segments; ++s)
+    hs[s] = CopySeg{static_cast<const char*>(src_bases[s]), static_cast<char*>(dst_bases[s]),
+                    page_bytes[s], 0};
+  PairDesc* hp = reinterpret_cast<PairDesc*>(h + pair_off);
+  for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_ids[i], dst_ids[i]};
+  char* dv = ctx->ring.dev + off;
+  hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
+  e = launch_copy(sh, vec, t.nt_stores != 0,
+                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg),
+                  sh.wg == 1024 && sh.chunk() >= (int64_t(32) << 10)
+                      ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
+                  stream, reinterpret_cast<const CopySeg*>(dv),
+                  reinterpret_cast<const PairDesc*>(dv + pair_off),
+                  static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),
+                  static_cast<uint32_t>(cpt));
+  if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
+  return ring_commit(ctx->ring, off, total, stream);
+}
+
 }  // namespace
 
 // =============================================================== C ABI ==
@@ -1064,93 +1184,23 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
                       const int64_t* dst_block_ids, hipStream_t stream) {
   g_err[0] = '\0';
   if (int rc = env_status()) return rc;
-  if (num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
-  if (!segment_bases || !segment_page_bytes)
+  return copy_core(num_segments, segment_bases, segment_bases, segment_page_bytes,
+                   device_num_blocks, device_num_blocks, num_pairs, src_block_ids,
+                   dst_block_ids, true, stream);
+}
+
+int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
+                         void* const* dst_segment_bases, const int64_t* segment_page_bytes,
+                         int64_t src_num_blocks, int64_t dst_num_blocks, int64_t num_pairs,
+                         const int64_t* src_block_ids, const int64_t* dst_block_ids,
+                         hipStream_t stream) {
+  g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
+  if (!src_segment_bases || !dst_segment_bases)
     return fail(AEGKV_EINVAL, "segment arrays must not be null");
-  if (device_num_blocks <= 0) return fail(AEGKV_EINVAL, "device_num_blocks must be positive");
-  if (num_pairs < 0) return fail(AEGKV_EINVAL, "num_pairs must be >= 0");
-  if (num_pairs > 0 && (!src_block_ids || !dst_block_ids))
-    return fail(AEGKV_EINVAL, "block id arrays must not be null");
-  bool vec = true;
-  int64_t max_page = 0;
-  for (int32_t s = 0; s < num_segments; ++s) {
-    if (!segment_bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
-    if (segment_page_bytes[s] <= 0)
-      return fail(AEGKV_EINVAL, "segment %d page_bytes must be positive", s);
-    if (!mul_fits(device_num_blocks, segment_page_bytes[s]))
-      return fail(AEGKV_ERANGE, "segment %d of %lld x %lld bytes overflows", s,
-                  static_cast<long long>(device_num_blocks),
-                  static_cast<long long>(segment_page_bytes[s]));
-    vec = vec && aligned16(segment_bases[s]) && segment_page_bytes[s] % 16 == 0;
-    max_page = std::max(max_page, segment_page_bytes[s]);
-  }
-  // 0 = untouched, 1 = source, 2 = target
-  std::vector<uint8_t> role(static_cast<size_t>(device_num_blocks), 0);
-  for (int64_t i = 0; i < num_pairs; ++i) {
-    const int64_t s = src_block_ids[i], d = dst_block_ids[i];
-    if (s < 0 || s >= device_num_blocks || d < 0 || d >= device_num_blocks)
-      return fail(AEGKV_ERANGE, "pair %lld (%lld -> %lld) outside [0, %lld)",
-                  static_cast<long long>(i), static_cast<long long>(s),
-                  static_cast<long long>(d), static_cast<long long>(device_num_blocks));
-    if (role[static_cast<size_t>(d)] == 2)
-      return fail(AEGKV_EDUP, "target block id %lld appears twice", static_cast<long long>(d));
-    if (role[static_cast<size_t>(d)] == 1)
-      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
-                  static_cast<long long>(d));
-    role[static_cast<size_t>(d)] = 2;
-  }
-  for (int64_t i = 0; i < num_pairs; ++i) {
-    const int64_t s = src_block_ids[i];
-    if (role[static_cast<size_t>(s)] == 2)
-      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
-                  static_cast<long long>(s));
-    role[static_cast<size_t>(s)] = 1;
-  }
-  if (num_pairs == 0) return 0;
-  for (int32_t s = 0; s < num_segments; ++s) {
-    int rc = check_device_range(segment_bases[s], device_num_blocks * segment_page_bytes[s],
-                                "segment base");
-    if (rc) return rc;
-  }
-  const Tunables t = tunables();
-  ShapeSel sh = auto_shape(max_page);
-  if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};
-  if (!vec) sh = ShapeSel{256, 1};
-  const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
-  const int64_t items = num_pairs * num_segments * cpt;
-  if (items >= (int64_t(1) << 32))
-    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
-                static_cast<long long>(items));
-  DeviceCtx* ctx = nullptr;
-  int rc = get_ctx(&ctx);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(ctx->mu);
-  const size_t seg_bytes = sizeof(SegDesc) * num_segments;
-  const size_t pair_off = (seg_bytes + 255) & ~size_t(255);
-  const size_t total = pair_off + sizeof(PairDesc) * num_pairs;
-  size_t off = 0;
-  rc = ring_reserve(ctx->ring, total, &off);
-  if (rc) return rc;
-  char* h = ctx->ring.host + off;
-  SegDesc* hs = reinterpret_cast<SegDesc*>(h);
-  for (int32_t s = 0; s < num_segments; ++s)
-    hs[s] = SegDesc{static_cast<char*>(segment_bases[s]), segment_page_bytes[s], 0, ~0ull};
-  PairDesc* hp = reinterpret_cast<PairDesc*>(h + pair_off);
-  for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_block_ids[i], dst_block_ids[i]};
-  char* dv = ctx->ring.dev + off;
-  hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
-  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
-  e = launch_copy(sh, vec, t.nt_stores != 0,
-                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg),
-                  sh.wg == 1024 && sh.chunk() >= (int64_t(32) << 10)
-                      ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
-                  stream,
-                  reinterpret_cast<const SegDesc*>(dv),
-                  reinterpret_cast<const PairDesc*>(dv + pair_off),
-                  static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),
-                  static_cast<uint32_t>(cpt));
-  if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
-  return ring_commit(ctx->ring, off, total, stream);
+  return copy_core(num_segments, src_segment_bases, dst_segment_bases, segment_page_bytes,
+                   src_num_blocks, dst_num_blocks, num_pairs, src_block_ids, dst_block_ids,
+                   false, stream);
 }
 
 int aegkv_host_alloc(void** ptr, int64_t bytes) { return aegkv_host_alloc_flags(ptr, bytes, 0); }

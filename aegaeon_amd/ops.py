@@ -298,6 +298,57 @@ def copy_blocks(
     _lib.check(rc)
 
 
+def migrate_blocks(
+    src_segments: Sequence[torch.Tensor],
+    dst_segments: Sequence[torch.Tensor],
+    src_block_ids,
+    dst_block_ids,
+    *,
+    segment_page_bytes: Sequence[int] | None = None,
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """Whole-block copy from one cache to another of the same layout:
+    dst_segments[s][dst[i]] := src_segments[s][src[i]] (aegkv_migrate_blocks).
+
+    The reference plans this move (aegaeon/block_manager.py:1527-1601,
+    aegaeon/worker.py:2420-2445) but leaves it unimplemented. The source
+    tensors may be another engine's cache on this GPU, tensors received from
+    another process (torch.multiprocessing, a HIP IPC memory handle), or a
+    peer GPU's cache with peer access enabled; the work runs on the target
+    cache's device. Each segment is viewed as [num_blocks, page] bytes; by
+    default the page is the tensor's bytes / size(0), equal for both caches.
+    """
+    if not src_segments or len(src_segments) != len(dst_segments):
+        raise ValueError("one source and one target tensor per segment are required")
+    dev = dst_segments[0].device
+    for i, (a, b) in enumerate(zip(src_segments, dst_segments)):
+        _require_device(a, f"source segment {i}")
+        _require_device(b, f"target segment {i}")
+        if b.device != dev:
+            raise ValueError("all target segments must live on one device")
+    n_src = src_segments[0].size(0)
+    n_dst = dst_segments[0].size(0)
+    if segment_page_bytes is None:
+        segment_page_bytes = [_tensor_bytes(t) // n_dst for t in dst_segments]
+    page = _i64(segment_page_bytes)
+    if page.size != len(dst_segments):
+        raise ValueError("segment_page_bytes must have one entry per segment")
+    for i, (a, b) in enumerate(zip(src_segments, dst_segments)):
+        if _tensor_bytes(a) < int(page[i]) * n_src or _tensor_bytes(b) < int(page[i]) * n_dst:
+            raise ValueError(f"segment {i} is smaller than its block count x page")
+    src = _i64(src_block_ids)
+    dst = _i64(dst_block_ids)
+    if src.shape != dst.shape:
+        raise ValueError("src and dst id lists differ in length")
+    sb = (ctypes.c_void_p * len(src_segments))(*[t.data_ptr() for t in src_segments])
+    db = (ctypes.c_void_p * len(dst_segments))(*[t.data_ptr() for t in dst_segments])
+    lib = _lib.load()
+    rc = _call_on(dev, lambda: lib.aegkv_migrate_blocks(
+        len(dst_segments), sb, db, _p64(page), int(n_src), int(n_dst), src.size, _p64(src),
+        _p64(dst), _stream_ptr(dev, stream)))
+    _lib.check(rc)
+
+
 def _free_pinned(ptr: int) -> None:
     rc = _lib.load().aegkv_host_free(ptr)
     if rc:

@@ -385,7 +385,12 @@ class SwapPlan:
 
     @property
     def is_swap_in(self) -> bool:
-        return is_gpu(self.target_location)
+        return is_gpu(self.target_location) and not is_gpu(self.source_location)
+
+    @property
+    def is_migration(self) -> bool:
+        """GPU engine -> GPU engine (whole blocks, no host pages)."""
+        return is_gpu(self.target_location) and is_gpu(self.source_location)
 
     @property
     def engine_id(self) -> int:
@@ -474,5 +479,64 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
     return plan
 
 
-__all__ = ["BLOCK_LOCATION_CPU", "BlockPools", "MoveRecord", "SwapPlan", "plan_move",
-           "slab_range"]
+def plan_migrate(requests: Sequence[int], block_tables: Dict[int, BlockTable],
+                 target_location: int, pools: BlockPools) -> Optional[SwapPlan]:
+    """Plan moving requests' blocks from one GPU engine to another
+    (BlockManager._migrate_requests, block_manager.py:1527-1601, which the
+    reference declares but leaves unimplemented).
+
+    Every moved request must sit on one source engine with one block shape,
+    and the target engine must use the tables' cache groups. Each request's
+    flat (non-released) blocks get fresh target ids in one allocation; the
+    table keeps its released columns (replace_flat_blocks) and moves to the
+    target. The returned plan lists whole blocks: source_block_ids on the
+    source engine, target_block_ids on the target engine, and all source ids
+    to free once the copy has finished (BlockPools.record_move). Returns
+    None when nothing moves.
+    """
+    if not is_gpu(target_location):
+        raise ValueError("migration targets a GPU engine; use plan_move for the host")
+    seen = set()
+    tables: List[Tuple[int, BlockTable]] = []
+    src_loc: Optional[int] = None
+    shape: Optional[Tuple[int, ...]] = None
+    for rid in requests:
+        if rid in seen:
+            continue
+        seen.add(rid)
+        table = block_tables.get(rid)
+        if table is None:
+            raise KeyError(f"request {rid} not allocated")
+        if table.location == target_location:
+            continue
+        if not is_gpu(table.location):
+            raise ValueError(f"request {rid} is on the host; migration moves GPU blocks")
+        if src_loc is not None and table.location != src_loc:
+            raise ValueError(f"request {rid} is on {table.location}; expected {src_loc}")
+        if shape is not None and tuple(table.block_shape) != shape:
+            raise ValueError(f"request {rid}'s shape is not {shape}")
+        if tuple(table.cache_groups) != pools.gpu_cache_groups.get(target_location):
+            raise ValueError(
+                f"request {rid} cache groups do not match target engine #{target_location}")
+        src_loc = table.location
+        shape = tuple(table.block_shape)
+        tables.append((rid, table))
+    if not tables:
+        return None
+    old = [table.blocks for _, table in tables]
+    targets = pools.allocate(sum(len(b) for b in old), target_location, shape)
+    plan = SwapPlan([rid for rid, _ in tables], src_loc, target_location, shape)
+    cursor = 0
+    for (_, table), blocks in zip(tables, old):
+        new = targets[cursor:cursor + len(blocks)]
+        cursor += len(blocks)
+        table.replace_flat_blocks(new)
+        table.location = target_location
+        plan.source_block_ids += blocks
+        plan.target_block_ids += new
+    plan.release_source_block_ids = list(plan.source_block_ids)
+    return plan
+
+
+__all__ = ["BLOCK_LOCATION_CPU", "BlockPools", "MoveRecord", "SwapPlan", "plan_migrate",
+           "plan_move", "slab_range"]

@@ -138,6 +138,9 @@ class KVSwapper:
         self._fence_count = [0, 0]
         self._fence_timed_out = torch.zeros(2, dtype=torch.int64, device=device)
         self.last_fence: Optional[FenceToken] = None
+        # other engines' caches this worker can migrate blocks from
+        self._own_pages = [cache.segment_pages(i) for i in range(len(cache.segments))]
+        self.peer_caches: Dict[int, List[torch.Tensor]] = {}
 
     def swap_blocks(self, request_ids: Sequence[int], source_block_ids: Sequence[int],
                     target_block_ids: Sequence[int], group_ids: Sequence[int],
@@ -165,13 +168,35 @@ class KVSwapper:
         if groups.size and (groups.min() < 0 or groups.max() >= len(self.group_descriptors)):
             bad = groups[(groups < 0) | (groups >= len(self.group_descriptors))][0]
             raise ValueError(f"Invalid swap cache-group id {int(bad)}")
-        if len(source_events) != len(request_ids):
-            raise ValueError("one source event slot per request is required")
         stream = self.swap_in_stream if is_swap_in else self.swap_out_stream
         new_event = torch.cuda.Event(interprocess=self.interprocess_events)
         # wait for in-flight moves of the same requests (worker.py:2351-2394);
         # bytes are IPC handles exported by another process
         side = 1 if is_swap_in else 0
+        self._wait_sources(request_ids, source_events, stream, side, new_event)
+        self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
+                          first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
+                          stream=stream)
+        new_event.record(stream)
+        self._signal(side, stream)
+        if logger.isEnabledFor(logging.INFO):
+            valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
+            copied = int((valid * self._bytes_per_kb[groups]).sum()) if groups.size else 0
+            extents = int(((valid > 0) * self._extents_per_entry[groups]).sum()) if groups.size else 0
+            full = len(source_block_ids) * self.cache.page_size_bytes
+            saved = 0.0 if full == 0 else 1.0 - copied / full
+            logger.info("swap requests %s (%s to %s): copied %d/%d bytes (saved %.2f%%), "
+                        "%d extents in one launch", list(request_ids),
+                        "CPU" if is_swap_in else "GPU", "GPU" if is_swap_in else "CPU",
+                        copied, full, saved * 100, extents)
+        return new_event
+
+    def _wait_sources(self, request_ids, source_events, stream, side: int,
+                      new_event: torch.cuda.Event) -> None:
+        """Order `stream` after the requests' previous moves
+        (worker.py:2351-2394): local events, IPC event handles or fences."""
+        if len(source_events) != len(request_ids):
+            raise ValueError("one source event slot per request is required")
         for rid, ev in zip(request_ids, source_events):
             if ev is not None:
                 if isinstance(ev, FenceToken):
@@ -184,25 +209,61 @@ class KVSwapper:
                         ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
                     stream.wait_event(ev)
             self.move_event_table[rid].append(new_event)
-        self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
-                          first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
-                          stream=stream)
-        new_event.record(stream)
+
+    def _signal(self, side: int, stream) -> None:
         if self.fence_slots is not None:
             self._fence_count[side] += 1
             ops.fence_signal(self.fence_words, self.fence_slots[side], self._fence_count[side],
                              stream=stream)
             self.last_fence = FenceToken(self.fence_slots[side], self._fence_count[side])
-        if logger.isEnabledFor(logging.INFO):
-            valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
-            copied = int((valid * self._bytes_per_kb[groups]).sum()) if groups.size else 0
-            extents = int(((valid > 0) * self._extents_per_entry[groups]).sum()) if groups.size else 0
-            full = len(source_block_ids) * self.cache.page_size_bytes
-            saved = 0.0 if full == 0 else 1.0 - copied / full
-            logger.info("swap requests %s (%s to %s): copied %d/%d bytes (saved %.2f%%), "
-                        "%d extents in one launch", list(request_ids),
-                        "CPU" if is_swap_in else "GPU", "GPU" if is_swap_in else "CPU",
-                        copied, full, saved * 100, extents)
+
+    def register_peer_cache(self, engine_id: int, segment_pages: Sequence[torch.Tensor]) -> None:
+        """Make another engine's cache a migration source
+        (Worker.register_kvcache_mem_handles, worker.py:2439-2445).
+
+        segment_pages: that cache's segments as [num_blocks, page] uint8
+        tensors in segment order, e.g. received from its process through
+        torch.multiprocessing (HIP IPC memory) or CompositeCache.segment_pages
+        of a cache in this process. Pages must match this cache's.
+        """
+        pages = list(segment_pages)
+        if len(pages) != len(self._own_pages):
+            raise ValueError(f"peer cache has {len(pages)} segments, expected "
+                             f"{len(self._own_pages)}")
+        for i, (p, own) in enumerate(zip(pages, self._own_pages)):
+            if p.dim() != 2 or p.size(1) != own.size(1) or p.dtype != torch.uint8:
+                raise ValueError(f"peer segment {i} must be uint8 [blocks, {own.size(1)}]")
+            if p.size(0) != pages[0].size(0):
+                raise ValueError("peer segments disagree on the block count")
+        self.peer_caches[engine_id] = pages
+
+    def unregister_peer_cache(self, engine_id: int) -> None:
+        """Worker.unregister_kvcache_mem_handles (worker.py:2447-2451)."""
+        self.peer_caches.pop(engine_id, None)
+
+    def migrate_blocks(self, request_ids: Sequence[int], source_engine_id: int,
+                       source_block_ids: Sequence[int], target_block_ids: Sequence[int],
+                       source_events: Sequence[Optional[Union[torch.cuda.Event, bytes,
+                                                              "FenceToken"]]]
+                       ) -> torch.cuda.Event:
+        """Copy whole blocks from a registered peer cache into this cache
+        (Worker.migrate_blocks, worker.py:2420-2430, unimplemented upstream).
+
+        Runs on the swap-in stream after the requests' previous moves, one
+        aegkv_migrate_blocks launch; returns the completion event and, with
+        fences configured, publishes last_fence for the swap-in word.
+        """
+        if source_engine_id not in self.peer_caches:
+            raise KeyError(f"engine {source_engine_id}'s cache is not registered")
+        if len(source_block_ids) != len(target_block_ids):
+            raise ValueError("source and target block lists differ in length")
+        stream = self.swap_in_stream
+        new_event = torch.cuda.Event(interprocess=self.interprocess_events)
+        self._wait_sources(request_ids, source_events, stream, 1, new_event)
+        ops.migrate_blocks(self.peer_caches[source_engine_id], self._own_pages,
+                           source_block_ids, target_block_ids, stream=stream)
+        new_event.record(stream)
+        self._signal(1, stream)
         return new_event
 
     @staticmethod

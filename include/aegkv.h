@@ -40,7 +40,8 @@ extern "C" {
 #define AEGKV_ERANGE (-2)        /* block id / group id outside its pool     */
 #define AEGKV_EDUP (-3)          /* a target block id appears twice          */
 #define AEGKV_EEXTENT (-4)       /* kernel-block extent outside the page     */
-#define AEGKV_EOVERLAP (-5)      /* copy_blocks: a source is also a target   */
+#define AEGKV_EOVERLAP (-5)      /* copy: a source is also a target, or the
+                                    migration's two caches overlap          */
 #define AEGKV_ENOMEM (-6)        /* descriptor larger than the upload ring   */
 
 /* host-transfer designs for swap-out / swap-in */
@@ -53,8 +54,8 @@ extern "C" {
 /* Environment, read once per process before the first call:
  *   AEGKV_AUTO_D2H, AEGKV_AUTO_H2D = direct | staged   (what AUTO picks)
  *   AEGKV_STAGING_BYTES = integer >= 1048576           (STAGED chunk)
- * An invalid value makes aegkv_swap, aegkv_swap_blocks and
- * aegkv_copy_blocks return AEGKV_EINVAL with a message naming it. */
+ * An invalid value makes aegkv_swap, aegkv_swap_blocks, aegkv_copy_blocks
+ * and aegkv_migrate_blocks return AEGKV_EINVAL with a message naming it. */
 
 /* tuning keys for aegkv_tune (values < 0 query without changing) */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS 1 /* swap-out kernel: workgroups    */
@@ -160,6 +161,29 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
                       int64_t device_num_blocks, int64_t num_pairs,
                       const int64_t* src_block_ids,
                       const int64_t* dst_block_ids, hipStream_t stream);
+
+/*
+ * Block migration between two caches of the same layout: for every segment
+ * s and pair i,
+ *   dst_seg_s[dst[i]] := src_seg_s[src[i]]   (one whole block).
+ * The reference declares migration but leaves it unimplemented:
+ * BlockManager._migrate_requests (aegaeon/block_manager.py:1527-1601) and
+ * Worker.migrate_blocks / migrate_blocks_source / register_kvcache_mem_handles
+ * (aegaeon/worker.py:2420-2445) raise NotImplementedError; their plan is
+ * that the target engine's worker copies whole blocks out of the source
+ * engine's cache, opened through IPC memory handles. Here the source
+ * segments may be any device memory the current device can read: another
+ * cache on this GPU, memory opened with hipIpcOpenMemHandle, or a peer
+ * GPU's memory over xGMI once peer access is enabled. Targets must be
+ * distinct (AEGKV_EDUP); the two caches must not overlap (AEGKV_EOVERLAP;
+ * use aegkv_copy_blocks within one cache). Same kernel and launch shape as
+ * aegkv_copy_blocks.
+ */
+int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
+                         void* const* dst_segment_bases, const int64_t* segment_page_bytes,
+                         int64_t src_num_blocks, int64_t dst_num_blocks, int64_t num_pairs,
+                         const int64_t* src_block_ids, const int64_t* dst_block_ids,
+                         hipStream_t stream);
 
 /*
  * Transfer entries of many block tables in one call (host-only; no GPU).

@@ -917,6 +917,117 @@ def test_swap_waits_on_ipc_event_from_another_process(gpu):
     pool.free()
 
 
+# --------------------------------------------------------------- migration --
+
+def test_migrate_blocks_between_caches_vs_expectation(gpu):
+    """aegkv_migrate_blocks copies whole blocks between two caches with the
+    same pages (one tile shape per segment, unaligned pages included);
+    everything else in both caches stays as it was."""
+    rng = np.random.default_rng(61)
+    pages = [160 * 1024, 32 * 1024, 4100, 100]
+    n_src, n_dst, n = 24, 20, 12
+    src_np = [rng.integers(0, 256, (n_src, p), dtype=np.uint8) for p in pages]
+    dst_np = [rng.integers(0, 256, (n_dst, p), dtype=np.uint8) for p in pages]
+    src = [torch.from_numpy(x.copy()).to(gpu) for x in src_np]
+    dst = [torch.from_numpy(x.copy()).to(gpu) for x in dst_np]
+    s_ids = rng.integers(0, n_src, n)                     # a source may repeat
+    d_ids = rng.permutation(n_dst)[:n]
+    _say("migrate blocks, pages", pages)
+    ops.migrate_blocks(src[:2], dst[:2], s_ids, d_ids)    # vector path
+    ops.migrate_blocks(src[2:], dst[2:], s_ids, d_ids)    # byte path (unaligned pages)
+    ops.migrate_blocks(src, dst, [], [])
+    torch.cuda.synchronize()
+    for k in range(len(pages)):
+        want = dst_np[k].copy()
+        want[d_ids] = src_np[k][s_ids]
+        assert np.array_equal(dst[k].cpu().numpy(), want), k
+        assert np.array_equal(src[k].cpu().numpy(), src_np[k]), k
+    with pytest.raises(ValueError, match="overlap"):
+        ops.migrate_blocks(src, src, [0], [1])
+
+
+def test_engine_to_engine_migration_through_planner(gpu):
+    """plan_migrate -> KVSwapper.migrate_blocks from a registered peer cache
+    -> record_move: the requests' blocks arrive whole at their new ids."""
+    from aegaeon_amd.cache_groups import CacheGroupConfig, CacheGroupRuntimeConfig, BlockTable
+    from aegaeon_amd.layout import allocate_composite_cache, kv_tensor_specs
+    from aegaeon_amd.planner import BlockPools, plan_migrate
+    from aegaeon_amd.swapper import KVSwapper
+
+    n_blocks = 96
+    specs = kv_tensor_specs(2, n_blocks, 16, 2, 64, 2)
+    caches = [allocate_composite_cache(specs, n_blocks, gpu) for _ in range(2)]
+    for t in caches[0].backing:
+        t.random_(-128, 127)
+    names = [{f"layers.{l}.{kv}" for l in range(2) for kv in ("k", "v")}]
+    descr = [CacheGroupRuntimeConfig("attention", 16, 16)]
+    groups = (CacheGroupConfig("attention", 16, 16),)
+    shape = (caches[0].page_size_bytes // 2,)
+    pools = BlockPools(2, 1 << 20)
+    for e in range(2):
+        pools.register_gpu_space(e, n_blocks, shape, groups)
+    pools.gpu_free_blocks[1].reverse()                    # scatter the target ids
+    host = ops.PinnedHostPool(4 * caches[0].page_size_bytes)
+    sw = [KVSwapper(c, names, descr, host.tensor) for c in caches]
+    sw[1].register_peer_cache(0, [caches[0].segment_pages(i) for i in range(4)])
+    tables = {r: BlockTable(0, shape, groups, [pools.allocate(5 + r, 0, shape)]) for r in range(6)}
+    before = {r: [caches[0].segment_pages(i)[tables[r].blocks].clone() for i in range(4)]
+              for r in tables}
+    plan = plan_migrate(list(tables), tables, 1, pools)
+    ev = sw[1].migrate_blocks(plan.request_ids, 0, plan.source_block_ids, plan.target_block_ids,
+                              [None] * len(plan.request_ids))
+    pools.record_move(plan, [ev])
+    ev.synchronize()
+    for r, table in tables.items():
+        assert table.location == 1
+        for i in range(4):
+            assert torch.equal(caches[1].segment_pages(i)[table.blocks], before[r][i]), (r, i)
+    assert pools.reclaim_gpu_moves(0, wait=False) == (1, len(plan.source_block_ids))
+    with pytest.raises(KeyError):
+        sw[0].migrate_blocks([0], 7, [1], [2], [None])
+    sw[1].unregister_peer_cache(0)
+    host.free()
+
+
+def _cache_owner(q_in, q_out):
+    """Child process: own a cache, fill it, hand its segments out through
+    torch IPC and keep them open until told to stop."""
+    import torch
+
+    torch.cuda.set_device(0)
+    pages = [torch.randint(0, 256, (32, p), dtype=torch.uint8, device="cuda")
+             for p in (65536, 16384)]
+    torch.cuda.synchronize()
+    q_out.put(pages)
+    q_in.get()
+
+
+def test_migrate_from_another_process_cache(gpu):
+    """A cache owned by another process, opened through IPC memory handles,
+    is a migration source (the reference's register_kvcache_mem_handles +
+    migrate_blocks plan, worker.py:2420-2445)."""
+    _say("migration from another process's cache")
+    mp = torch.multiprocessing.get_context("spawn")
+    q_in, q_out = mp.Queue(), mp.Queue()
+    child = mp.Process(target=_cache_owner, args=(q_in, q_out), daemon=True)
+    child.start()
+    try:
+        peer = q_out.get(timeout=100)
+        own = [torch.zeros(40, p.size(1), dtype=torch.uint8, device=gpu) for p in peer]
+        s_ids, d_ids = np.arange(3, 19), np.arange(39, 23, -1)
+        ops.migrate_blocks(peer, own, s_ids, d_ids)
+        torch.cuda.synchronize()
+        for p, o in zip(peer, own):
+            assert torch.equal(o[torch.from_numpy(d_ids).to(gpu)], p[torch.from_numpy(s_ids).to(gpu)])
+            assert int(o[:23].count_nonzero()) == 0
+        del peer
+    finally:
+        q_in.put(None)
+        child.join(60)
+        if child.is_alive():
+            child.kill()
+
+
 # ------------------------------------------------------------------ fences --
 
 def _busy(n_iter=200):

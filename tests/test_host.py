@@ -400,3 +400,29 @@ def test_host_alloc_flags_rejections(aegkv_lib):
     assert b"flags" in aegkv_lib.aegkv_last_error()
     assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 0, 1) == _lib.EINVAL
     assert aegkv_lib.aegkv_host_alloc_flags(None, 16, 1) == _lib.EINVAL
+
+
+def test_migrate_blocks_rejections_before_any_hip_call(aegkv_lib):
+    import ctypes
+
+    from aegaeon_amd import _lib
+
+    lib = aegkv_lib
+    A = (ctypes.c_void_p * 2)(0x10000000, 0x20000000)
+    B = (ctypes.c_void_p * 2)(0x30000000, 0x40000000)
+    page = np.array([4096, 4096], np.int64)
+    p64 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))  # noqa: E731
+
+    def call(src_b, dst_b, src, dst, n_src=8, n_dst=8, n_seg=2):
+        s, d = np.array(src, np.int64), np.array(dst, np.int64)
+        return lib.aegkv_migrate_blocks(n_seg, src_b, dst_b, p64(page), n_src, n_dst, s.size,
+                                        p64(s), p64(d), None)
+
+    assert call(A, B, [1], [2], n_seg=0) == _lib.EINVAL
+    assert call(None, B, [1], [2]) == _lib.EINVAL
+    assert call(A, A, [1], [2]) == _lib.EOVERLAP          # one cache: use copy_blocks
+    assert b"overlap" in lib.aegkv_last_error()
+    assert call(A, B, [8], [2]) == _lib.ERANGE            # source id past the source cache
+    assert call(A, B, [1], [3], n_dst=3) == _lib.ERANGE   # target id past the target cache
+    assert call(A, B, [1, 2], [5, 5]) == _lib.EDUP
+    assert call(A, B, [], []) == _lib.OK                   # nothing to move, no GPU needed

@@ -314,3 +314,53 @@ def test_reregistering_an_engine_settles_its_moves():
     assert len(pools.move_events_gpu[0]) == 0 and pools.move_gpu_num_blocks[0] == 0
     assert pools.gpu_free_blocks[0] == list(range(1, 20))
     assert sum(pools.cpu_slab_usage) == 8              # both requests on the host
+
+
+# ---------------------------------------------------------------- migration --
+
+def test_plan_migrate_moves_flat_blocks_and_keeps_released_columns():
+    from aegaeon_amd.planner import plan_migrate
+
+    pools = BlockPools(cpu_num_slabs=4, cpu_slab_size_bytes=1 << 16)
+    pools.register_gpu_space(0, 64, SHAPE, GROUPS)
+    pools.register_gpu_space(1, 64, SHAPE, GROUPS)
+    t0 = BlockTable(0, SHAPE, GROUPS, [pools.allocate(3, 0, SHAPE), pools.allocate(2, 0, SHAPE),
+                                       pools.allocate(1, 0, SHAPE)])
+    t0.group_blocks[1][0] = LOGICAL_NULL_BLOCK_ID          # a released window column
+    t1 = BlockTable(0, SHAPE, GROUPS, [pools.allocate(2, 0, SHAPE), [], pools.allocate(1, 0, SHAPE)])
+    tables = {0: t0, 1: t1}
+    old = [list(t0.blocks), list(t1.blocks)]
+    plan = plan_migrate([0, 1, 0], tables, 1, pools)
+    assert plan.is_migration and not plan.is_swap_in and plan.engine_id == 1
+    assert plan.source_block_ids == old[0] + old[1]
+    assert len(plan.target_block_ids) == len(plan.source_block_ids) == 8
+    assert plan.release_source_block_ids == plan.source_block_ids
+    assert t0.location == t1.location == 1
+    assert t0.group_blocks[1][0] == LOGICAL_NULL_BLOCK_ID
+    assert t0.blocks + t1.blocks == plan.target_block_ids
+    assert plan_migrate([0], tables, 1, pools) is None        # already there
+    pools.record_move(plan, [])
+    assert pools.move_gpu_num_blocks[0] == 8
+    assert pools.reclaim_gpu_moves(0, wait=False) == (1, 8)
+
+
+def test_plan_migrate_rejections():
+    from aegaeon_amd.planner import plan_migrate
+
+    pools = BlockPools(cpu_num_slabs=4, cpu_slab_size_bytes=1 << 16)
+    pools.register_gpu_space(0, 64, SHAPE, GROUPS)
+    pools.register_gpu_space(1, 64, SHAPE, GROUPS)
+    pools.register_gpu_space(2, 64, SHAPE, GROUPS[:1])
+    tables = {0: BlockTable(0, SHAPE, GROUPS, [[1], [2], [3]]),
+              1: BlockTable(BLOCK_LOCATION_CPU, SHAPE, GROUPS, [[4], [5], [6]]),
+              2: BlockTable(2, SHAPE, GROUPS[:1], [[7]])}
+    with pytest.raises(ValueError, match="GPU engine"):
+        plan_migrate([0], tables, BLOCK_LOCATION_CPU, pools)
+    with pytest.raises(ValueError, match="host"):
+        plan_migrate([1], tables, 1, pools)
+    with pytest.raises(ValueError, match="cache groups"):
+        plan_migrate([0], tables, 2, pools)
+    with pytest.raises(ValueError, match="expected"):
+        plan_migrate([0, 2], tables, 1, pools)
+    with pytest.raises(KeyError):
+        plan_migrate([9], tables, 1, pools)
