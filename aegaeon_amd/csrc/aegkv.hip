@@ -1243,7 +1243,8 @@ int aegkv_host_free(void* ptr) {
   {
     std::lock_guard<std::mutex> lk(g_host_mu);
     const uintptr_t b = reinterpret_cast<uintptr_t>(ptr);
-    g_host_allocs.erase(b);
+    if (g_host_allocs.erase(b) == 0)
+      return fail(AEGKV_EINVAL, "%p is not a live pool from aegkv_host_alloc", ptr);
     auto u = g_uncached.find(b);
     if (u != g_uncached.end()) {
       // uncached pools stay mapped until the process ends; a later uncached

@@ -145,7 +145,8 @@ class KVSwapper:
     def swap_blocks(self, request_ids: Sequence[int], source_block_ids: Sequence[int],
                     target_block_ids: Sequence[int], group_ids: Sequence[int],
                     first_kernel_blocks: Sequence[int], valid_kernel_blocks: Sequence[int],
-                    source_events: Sequence[Optional[Union[torch.cuda.Event, bytes]]],
+                    source_events: Sequence[Optional[Union[torch.cuda.Event, bytes,
+                                                           "FenceToken"]]],
                     is_swap_in: bool, mode="auto") -> torch.cuda.Event:
         """Move the live extents of some blocks between host and device.
 
@@ -173,12 +174,11 @@ class KVSwapper:
         # wait for in-flight moves of the same requests (worker.py:2351-2394);
         # bytes are IPC handles exported by another process
         side = 1 if is_swap_in else 0
-        self._wait_sources(request_ids, source_events, stream, side, new_event)
+        self._wait_sources(request_ids, source_events, stream, side)
         self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
                           first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
                           stream=stream)
-        new_event.record(stream)
-        self._signal(side, stream)
+        self._finish(request_ids, side, stream, new_event)
         if logger.isEnabledFor(logging.INFO):
             valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
             copied = int((valid * self._bytes_per_kb[groups]).sum()) if groups.size else 0
@@ -191,13 +191,12 @@ class KVSwapper:
                         copied, full, saved * 100, extents)
         return new_event
 
-    def _wait_sources(self, request_ids, source_events, stream, side: int,
-                      new_event: torch.cuda.Event) -> None:
+    def _wait_sources(self, request_ids, source_events, stream, side: int) -> None:
         """Order `stream` after the requests' previous moves
         (worker.py:2351-2394): local events, IPC event handles or fences."""
         if len(source_events) != len(request_ids):
             raise ValueError("one source event slot per request is required")
-        for rid, ev in zip(request_ids, source_events):
+        for ev in source_events:
             if ev is not None:
                 if isinstance(ev, FenceToken):
                     if self.fence_words is None:
@@ -208,7 +207,15 @@ class KVSwapper:
                     if isinstance(ev, (bytes, bytearray)):
                         ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
                     stream.wait_event(ev)
+
+    def _finish(self, request_ids, side: int, stream, new_event: torch.cuda.Event) -> None:
+        """Record the move's completion event behind the enqueued work, list
+        it for the requests (worker.py:2252-2257) and raise the stream's
+        fence word when fences are configured."""
+        new_event.record(stream)
+        for rid in request_ids:
             self.move_event_table[rid].append(new_event)
+        self._signal(side, stream)
 
     def _signal(self, side: int, stream) -> None:
         if self.fence_slots is not None:
@@ -259,11 +266,10 @@ class KVSwapper:
             raise ValueError("source and target block lists differ in length")
         stream = self.swap_in_stream
         new_event = torch.cuda.Event(interprocess=self.interprocess_events)
-        self._wait_sources(request_ids, source_events, stream, 1, new_event)
+        self._wait_sources(request_ids, source_events, stream, 1)
         ops.migrate_blocks(self.peer_caches[source_engine_id], self._own_pages,
                            source_block_ids, target_block_ids, stream=stream)
-        new_event.record(stream)
-        self._signal(1, stream)
+        self._finish(request_ids, 1, stream, new_event)
         return new_event
 
     @staticmethod

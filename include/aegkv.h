@@ -235,6 +235,9 @@ int aegkv_host_alloc(void** ptr, int64_t bytes);
  */
 #define AEGKV_HOST_UNCACHED 1
 int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags);
+/* Release a pool from aegkv_host_alloc(_flags); null is a no-op, any other
+ * pointer that is not a live pool (freed twice, or not from this library)
+ * is rejected with AEGKV_EINVAL. */
 int aegkv_host_free(void* ptr);
 
 /*

@@ -7,6 +7,7 @@ host pages equal to the device tiles they came from, untouched blocks
 unchanged.
 """
 
+import ctypes
 import itertools
 
 import numpy as np
@@ -419,6 +420,8 @@ def test_uncached_host_pool_vs_oracle(gpu, oracle, mode):
     first_pool.free()
     pool = ops.PinnedHostPool(n_host * composite, uncached=True)
     assert pool.tensor.data_ptr() == first_ptr          # parked memory reused
+    lib = _lib.load()
+    assert lib.aegkv_host_free(ctypes.c_void_p(first_ptr + 4096)) == _lib.EINVAL
     host_np = rng.integers(0, 256, (n_host, composite), dtype=np.uint8)
     pool.tensor.copy_(torch.from_numpy(host_np.reshape(-1)))
     grp = rng.integers(0, 3, n).astype(np.int32)
@@ -542,6 +545,26 @@ def test_rejections_enqueue_nothing(gpu):
     torch.cuda.synchronize()
     assert torch.equal(seg, before)
     assert bool((pool.tensor == 7).all())
+    pool.free()
+
+
+def test_rejected_swap_leaves_no_event_behind(gpu):
+    """A swap the library rejects raises before anything is recorded: the
+    request gets no completion event and the fence count does not move."""
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import KVSwapper
+
+    cache = allocate_composite_cache([KVCacheTensorSpec(8 * 4096, ("l0",))], 8, gpu)
+    pool = ops.PinnedHostPool(4 * 4096)
+    words = torch.zeros(2, dtype=torch.int64, device=gpu)
+    sw = KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
+                   fence_words=words, fence_slots=(0, 1))
+    with pytest.raises(ValueError, match="outside"):
+        sw.swap_blocks([3], [9], [0], [0], [0], [1], [None], False)   # device id 9 of 8
+    assert 3 not in sw.move_event_table and sw.last_fence is None
+    torch.cuda.synchronize()
+    assert int(words[0]) == 0
     pool.free()
 
 
