@@ -806,7 +806,12 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   const bool nt = t.nt_stores != 0 && !(!is_swap_in && !staged);
   const int64_t wgs = is_swap_in ? t.swap_in_workgroups : t.swap_out_workgroups;
   e = launch_swap(sh, !is_swap_in, vec, nt, launch_grid(wgs, items, sh.wg), stream, a);
-  if (e != hipSuccess) return hip_fail(e, "swap_tiles_kernel launch");
+  if (e != hipSuccess) {
+    // the descriptor upload is already enqueued: retire its region in order
+    (void)hipGetLastError();
+    (void)ring_commit(ctx->ring, off, total, stream);
+    return hip_fail(e, "swap_tiles_kernel launch");
+  }
   return ring_commit(ctx->ring, off, total, stream);
 }
 
@@ -1076,7 +1081,12 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
                   reinterpret_cast<const PairDesc*>(dv + pair_off),
                   static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),
                   static_cast<uint32_t>(cpt));
-  if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
+  if (e != hipSuccess) {
+    // the descriptor upload is already enqueued: retire its region in order
+    (void)hipGetLastError();
+    (void)ring_commit(ctx->ring, off, total, stream);
+    return hip_fail(e, "copy_blocks_kernel launch");
+  }
   return ring_commit(ctx->ring, off, total, stream);
 }
 
