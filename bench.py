@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-switch", action="store_true",
+                   help="skip the model-switch line (both link directions at once)")
     p.add_argument("--cpu-runs", type=int, default=5)
     p.add_argument("--no-reference-loop", action="store_true",
                    help="skip timing the reference per-extent copy loop on the GPU "
@@ -99,7 +101,10 @@ def measure_link(torch, ops, dev, nbytes=1 << 30, reps=3):
 
 
 def measure_link_bidir(torch, ops, dev, nbytes=4 << 30):
-    """Both directions at once (two streams), aggregate GB/s."""
+    """Both directions at once (two streams), aggregate GB/s. Measured
+    first thing in a process: later, once more streams share the process's
+    4 hardware queues, the two runtime copies were seen running one after
+    the other."""
     hp = [ops.PinnedHostPool(nbytes) for _ in range(2)]
     dv = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(2)]
     st = [torch.cuda.Stream() for _ in range(2)]
@@ -427,7 +432,9 @@ def bench_switch(args):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _lib.load()
-    bidir = measure_link_bidir(torch, ops, dev)   # before the swappers create their streams
+    bidir = getattr(args, "bidir", None)
+    if bidir is None:   # measured before the swappers create their streams
+        bidir = measure_link_bidir(torch, ops, dev)
     L, NB, H, D, NREQ = 28, 16384, 4, 128, 64
     specs = kv_tensor_specs(L, NB, 16, H, D, 2)
     names = [{f"layers.{l}.{kv}" for l in range(L) for kv in ("k", "v")}]
@@ -735,6 +742,7 @@ def main():
     _lib.load()
 
     log("measuring host-link and stream-copy ceilings")
+    bidir = None if args.no_switch else measure_link_bidir(torch, ops, dev)
     link = measure_link(torch, ops, dev)
     stream_copy = measure_stream_copy(torch, dev)
 
@@ -911,6 +919,19 @@ def main():
     pool.free()
     del segs1, segs2
     torch.cuda.empty_cache()
+    # Both link directions at once, as a token-level model switch drives
+    # them: planner + swapper + move ledger on two engines (see --config
+    # switch). Reported beside the metric, not part of `value`.
+    line["model_switch"] = None
+    if not args.no_switch:
+        log("model switch: two engines, swap-out and swap-in at once")
+        sw = bench_switch(argparse.Namespace(steps=5, warmup=1, bidir=bidir))
+        line["model_switch"] = {k: sw[k] for k in (
+            "switch_wall_ms", "host_plan_and_enqueue_ms", "bytes_per_switch",
+            "link_aggregate_GBps", "link_bidirectional_ceiling_GBps",
+            "frac_bidirectional_ceiling", "bit_exact")}
+        line["model_switch"]["workload"] = sw["config"]["workload"]
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (reference torch path on host tensors)")
         line["cpu_baseline"] = cpu_baseline(args.cpu_runs)
