@@ -113,6 +113,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     with _lock:
         if _lib is not None:
             return _lib
+        if path is None:
+            path = os.environ.get("AEGKV_LIBRARY") or None   # another build, e.g. sanitized
         p = Path(path) if path is not None else LIB_PATH
         if not p.exists():
             raise ImportError(
