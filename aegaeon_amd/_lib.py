@@ -60,6 +60,8 @@ EXPORTED_SYMBOLS = (
     "aegkv_host_free",
     "aegkv_fence_signal",
     "aegkv_fence_wait",
+    "aegkv_stream_create",
+    "aegkv_stream_destroy",
 )
 
 _P = ctypes.c_void_p
@@ -93,6 +95,8 @@ _SIGNATURES = {
     "aegkv_host_free": (_INT, [_P]),
     "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
     "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),
+    "aegkv_stream_create": (_INT, [_PP]),
+    "aegkv_stream_destroy": (_INT, [_P]),
 }
 
 _lib = None

@@ -843,6 +843,21 @@ void entry_runs(const SwapLayout& L, const SwapList& E, int64_t i, bool is_swap_
   }
 }
 
+// A stream on a hardware queue of its own: a stream created with a CU mask
+// gets a dedicated queue (here the mask enables every CU), while plain
+// streams share the process's GPU_MAX_HW_QUEUES queues, and two copies whose
+// streams share a queue run one after the other.
+hipError_t dedicated_stream(hipStream_t* out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  std::vector<uint32_t> mask(static_cast<size_t>((cus + 31) / 32), 0xFFFFFFFFu);
+  return hipExtStreamCreateWithCUMask(out, static_cast<uint32_t>(mask.size()), mask.data());
+}
+
 // Create the DMA streams and events once (caller holds the set's mutex).
 int ensure_dma(DeviceCtx::DmaSet& d, int k) {
   if (!d.fork_ev) AEGKV_HIP(hipEventCreateWithFlags(&d.fork_ev, hipEventDisableTiming));
@@ -1211,6 +1226,20 @@ int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
   return copy_core(num_segments, src_segment_bases, dst_segment_bases, segment_page_bytes,
                    src_num_blocks, dst_num_blocks, num_pairs, src_block_ids, dst_block_ids,
                    false, stream);
+}
+
+int aegkv_stream_create(hipStream_t* stream) {
+  g_err[0] = '\0';
+  if (!stream) return fail(AEGKV_EINVAL, "stream pointer must not be null");
+  AEGKV_HIP(dedicated_stream(stream));
+  return 0;
+}
+
+int aegkv_stream_destroy(hipStream_t stream) {
+  g_err[0] = '\0';
+  if (!stream) return fail(AEGKV_EINVAL, "stream must not be null");
+  AEGKV_HIP(hipStreamDestroy(stream));
+  return 0;
 }
 
 int aegkv_host_alloc(void** ptr, int64_t bytes) { return aegkv_host_alloc_flags(ptr, bytes, 0); }

@@ -349,6 +349,29 @@ def migrate_blocks(
     _lib.check(rc)
 
 
+class DedicatedStream:
+    """A HIP stream on a hardware queue of its own (aegkv_stream_create),
+    usable wherever torch takes a stream through `.stream`.
+
+    Plain streams (torch.cuda.Stream included) share the process's 4
+    hardware queues, and two streams on one queue run their work one after
+    the other; a swap-out and a swap-in on dedicated streams always overlap.
+    The stream is destroyed by close() or when the object is collected.
+    """
+
+    def __init__(self, device: torch.device | None = None):
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        lib = _lib.load()
+        ptr = ctypes.c_void_p()
+        _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create(ctypes.byref(ptr))))
+        self.device = dev
+        self.stream = torch.cuda.ExternalStream(ptr.value, device=dev)
+        self._fin = weakref.finalize(self, lib.aegkv_stream_destroy, ptr.value)
+
+    def close(self) -> None:
+        self._fin()
+
+
 def _free_pinned(ptr: int) -> None:
     rc = _lib.load().aegkv_host_free(ptr)
     if rc:

@@ -58,7 +58,7 @@ class KVSwapper:
                  host_element_size: int = 2, interprocess_events: bool = False,
                  fence_words: Optional[torch.Tensor] = None,
                  fence_slots: Optional[Tuple[int, int]] = None,
-                 fence_timeout_s: float = 30.0):
+                 fence_timeout_s: float = 30.0, dedicated_streams: bool = True):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -116,8 +116,16 @@ class KVSwapper:
             self._segments, self._page, self._cpu_off, self._owner_mask, cache.num_blocks,
             self._kpp, self.kv_swap_view.view(-1), self.host_page_bytes,
             self.tp_rank * cache.page_size_bytes)
-        self.swap_in_stream = torch.cuda.Stream(device)
-        self.swap_out_stream = torch.cuda.Stream(device)
+        # swap streams (worker.py:278-280), each on a hardware queue of its own
+        # so that a swap-in and a swap-out never wait for each other
+        if dedicated_streams:
+            self._streams = [ops.DedicatedStream(device), ops.DedicatedStream(device)]
+            self.swap_in_stream = self._streams[0].stream
+            self.swap_out_stream = self._streams[1].stream
+        else:
+            self._streams = []
+            self.swap_in_stream = torch.cuda.Stream(device)
+            self.swap_out_stream = torch.cuda.Stream(device)
         self.move_event_table: Dict[int, List[torch.cuda.Event]] = defaultdict(list)
         # fences: (swap-out word, swap-in word) this swapper raises; flags
         # its waits set on timeout, [swap-out stream, swap-in stream]

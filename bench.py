@@ -100,14 +100,33 @@ def measure_link(torch, ops, dev, nbytes=1 << 30, reps=3):
     return out
 
 
-def measure_link_bidir(torch, ops, dev, nbytes=4 << 30):
-    """Both directions at once (two streams), aggregate GB/s. Measured
-    first thing in a process: later, once more streams share the process's
-    4 hardware queues, the two runtime copies were seen running one after
-    the other."""
+def measure_link_bidir(torch, ops, dev, nbytes=4 << 30, retries=6):
+    """Both directions at once, aggregate GB/s: a D2H and an H2D runtime
+    copy started together on two streams with hardware queues of their own
+    (on streams that share a queue the copies run one after the other);
+    best of three runs.
+
+    Right after another GPU process has exited (a test run, say), the two
+    copies were seen running one after the other for some seconds (60 GB/s
+    instead of 97) while its queues were still being released; a result
+    below 1.25x one direction is measured again after 5 s, up to `retries`
+    times."""
+    best = _bidir_once(torch, ops, dev, nbytes)
+    for _ in range(retries):
+        if best > 1.25 * 57.0:
+            break
+        log(f"bidirectional copies ran one after the other ({best:.1f} GB/s); "
+            "measuring again in 5 s")
+        time.sleep(5)
+        best = max(best, _bidir_once(torch, ops, dev, nbytes))
+    return best
+
+
+def _bidir_once(torch, ops, dev, nbytes):
     hp = [ops.PinnedHostPool(nbytes) for _ in range(2)]
     dv = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(2)]
-    st = [torch.cuda.Stream() for _ in range(2)]
+    owners = [ops.DedicatedStream(dev) for _ in range(2)]
+    st = [o.stream for o in owners]
     best = 0.0
     for _ in range(3):
         begin = torch.cuda.Event(enable_timing=True)
@@ -128,6 +147,8 @@ def measure_link_bidir(torch, ops, dev, nbytes=4 << 30):
     del dv
     for h in hp:
         h.free()
+    for o in owners:
+        o.close()
     return best
 
 
@@ -198,21 +219,6 @@ def cpu_baseline(runs: int):
                    f"staging + scatter to 256 other ids = {moved} bytes; median of {runs} runs, "
                    f"torch threads 1 of os.cpu_count()={os.cpu_count()}; bit-exact round trip"),
     }
-
-
-def hip_streams(n):
-    """n new HIP streams from the HIP runtime torch loaded (hipStreamCreate)."""
-    import ctypes
-
-    hip = ctypes.CDLL("libamdhip64.so.7")
-    out = []
-    for _ in range(n):
-        p = ctypes.c_void_p()
-        rc = hip.hipStreamCreate(ctypes.byref(p))
-        if rc != 0:
-            raise RuntimeError(f"hipStreamCreate failed ({rc})")
-        out.append(p.value)
-    return out
 
 
 def ev_pair(torch):
@@ -309,7 +315,7 @@ def bench_overlap(args):
 
     dev = torch.device("cuda:0")
     _lib.load()
-    streams_raw = hip_streams(3)
+    owners = [ops.DedicatedStream(dev) for _ in range(3)]
     bidir = measure_link_bidir(torch, ops, dev)
     L, NB, H, D = 24, 32768, 16, 128
     NOUT, NIN, NP = 16384, 12288, 2048
@@ -346,10 +352,9 @@ def bench_overlap(args):
     for t in segs:
         t.index_fill_(0, di, 0)
     torch.cuda.synchronize()
-    # Three freshly created HIP streams (created before any other stream
-    # work of this run, so each gets its own hardware queue); three runs,
-    # the medians reported.
-    streams = [torch.cuda.ExternalStream(p) for p in streams_raw]
+    # Three streams with hardware queues of their own; three runs, the
+    # medians reported.
+    streams = [o.stream for o in owners]
     runs = []
     for _ in range(3):
         evs = [ev_pair(torch) for _ in range(3)]

@@ -214,6 +214,18 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
                            int64_t* out_first, int64_t* out_count, int64_t* num_rows);
 
 /*
+ * A stream on a hardware queue of its own, for the swap-in and swap-out
+ * streams the reference creates with torch.cuda.Stream()
+ * (aegaeon/worker.py:278-280). Plain HIP streams share the process's
+ * GPU_MAX_HW_QUEUES (4) hardware queues, and work on two streams that
+ * share a queue runs one after the other, so a swap-out and a swap-in
+ * can lose their overlap; a stream created with a CU mask gets a queue to
+ * itself (the mask here enables every CU). Default priority.
+ */
+int aegkv_stream_create(hipStream_t* stream);
+int aegkv_stream_destroy(hipStream_t stream);
+
+/*
  * Pinned host pool. Replaces the pinning half of the reference's host KV
  * pool set-up: Controller._init_cpu_cache (aegaeon/llm.py:1020-1040) and
  * the worker's cudaHostRegister of that mapping (aegaeon/worker.py:251-273).
