@@ -356,7 +356,8 @@ class DedicatedStream:
     Plain streams (torch.cuda.Stream included) share the process's 4
     hardware queues, and two streams on one queue run their work one after
     the other; a swap-out and a swap-in on dedicated streams always overlap.
-    The stream is destroyed by close() or when the object is collected.
+    The HIP stream lives while this object or its `.stream` is referenced
+    and is destroyed by close() or when both are gone.
     """
 
     def __init__(self, device: torch.device | None = None):
@@ -366,6 +367,9 @@ class DedicatedStream:
         _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create(ctypes.byref(ptr))))
         self.device = dev
         self.stream = torch.cuda.ExternalStream(ptr.value, device=dev)
+        # the stream object keeps its owner alive, so `.stream` alone is
+        # enough to hold the HIP stream
+        self.stream._aegkv_owner = self
         self._fin = weakref.finalize(self, lib.aegkv_stream_destroy, ptr.value)
 
     def close(self) -> None:

@@ -1051,6 +1051,25 @@ def test_migrate_from_another_process_cache(gpu):
             child.kill()
 
 
+def test_dedicated_stream_lives_with_its_torch_stream(gpu):
+    """A DedicatedStream's `.stream` keeps the HIP stream alive after the
+    owner object is dropped; work on it completes and orders normally."""
+    import gc
+
+    st = ops.DedicatedStream(gpu).stream
+    gc.collect()
+    x = torch.arange(1 << 20, device=gpu, dtype=torch.int32)
+    with torch.cuda.stream(st):
+        y = x * 3
+        done = torch.cuda.Event()
+        done.record(st)
+    torch.cuda.current_stream().wait_event(done)
+    assert int((y - 3 * x).abs().sum()) == 0
+    owner = st._aegkv_owner
+    del st
+    owner.close()                                   # explicit release is also fine
+
+
 # ------------------------------------------------------------------ fences --
 
 def _busy(n_iter=200):
