@@ -356,6 +356,9 @@ class DedicatedStream:
     Plain streams (torch.cuda.Stream included) share the process's 4
     hardware queues, and two streams on one queue run their work one after
     the other; a swap-out and a swap-in on dedicated streams always overlap.
+    Unlike torch's pool streams, a dedicated stream is a blocking stream: it
+    synchronizes with the legacy default (null) stream, so work on it waits
+    for the default stream's earlier work and the other way round.
     The HIP stream lives while this object or its `.stream` is referenced
     and is destroyed by close() or when both are gone.
     """

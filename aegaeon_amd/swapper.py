@@ -58,7 +58,7 @@ class KVSwapper:
                  host_element_size: int = 2, interprocess_events: bool = False,
                  fence_words: Optional[torch.Tensor] = None,
                  fence_slots: Optional[Tuple[int, int]] = None,
-                 fence_timeout_s: float = 30.0, dedicated_streams: bool = True):
+                 fence_timeout_s: float = 30.0, dedicated_streams: bool = False):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -116,8 +116,12 @@ class KVSwapper:
             self._segments, self._page, self._cpu_off, self._owner_mask, cache.num_blocks,
             self._kpp, self.kv_swap_view.view(-1), self.host_page_bytes,
             self.tp_rank * cache.page_size_bytes)
-        # swap streams (worker.py:278-280), each on a hardware queue of its own
-        # so that a swap-in and a swap-out never wait for each other
+        # swap streams (worker.py:278-280). Plain torch streams share the
+        # process's 4 hardware queues (two swaps on one queue run back to
+        # back). dedicated_streams=True gives each its own queue, but such
+        # streams also synchronize with the legacy default (null) stream, so
+        # they suit processes whose other GPU work runs on non-default
+        # streams.
         if dedicated_streams:
             self._streams = [ops.DedicatedStream(device), ops.DedicatedStream(device)]
             self.swap_in_stream = self._streams[0].stream

@@ -465,7 +465,9 @@ def bench_switch(args):
         pools.register_gpu_space(e, NB, shape, groups)
         free = pools.gpu_free_blocks[e]
         free[:] = list(rng.permutation(free))
-        sw.append(KVSwapper(caches[e], names, descr, host.tensor))
+        # dedicated streams: nothing else runs on the GPU here, and the
+        # swap-out and swap-in never land on one hardware queue
+        sw.append(KVSwapper(caches[e], names, descr, host.tensor, dedicated_streams=True))
     tables, reqs = {}, [[], []]
     for e in range(2):
         for i, tok in enumerate(lengths[e]):

@@ -220,7 +220,8 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
  * GPU_MAX_HW_QUEUES (4) hardware queues, and work on two streams that
  * share a queue runs one after the other, so a swap-out and a swap-in
  * can lose their overlap; a stream created with a CU mask gets a queue to
- * itself (the mask here enables every CU). Default priority.
+ * itself (the mask here enables every CU). Default priority. It is a
+ * blocking stream: it synchronizes with the legacy default (null) stream.
  */
 int aegkv_stream_create(hipStream_t* stream);
 int aegkv_stream_destroy(hipStream_t stream);
