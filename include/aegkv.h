@@ -21,6 +21,9 @@
  *     calling thread's most recent failure.
  *   - The caller keeps every buffer alive until the stream has passed the
  *     enqueued work (record an event after the call and wait on it).
+ *   - Calls are not for stream capture (hipGraph): their descriptors are
+ *     uploaded from a host ring at enqueue time, which a graph replay would
+ *     not repeat.
  */
 #ifndef AEGKV_H
 #define AEGKV_H
