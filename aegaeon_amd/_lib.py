@@ -43,6 +43,7 @@ TUNE_SWAP_IN_WORKGROUPS = 9
 TUNE_STAGED_DMA_STREAMS = 10
 TUNE_COPY_LDS_BYTES = 11
 TUNE_SWAP_UNROLL = 12
+TUNE_STAGED_WORKGROUPS = 13
 HOST_UNCACHED = 1
 
 #: every symbol include/aegkv.h declares

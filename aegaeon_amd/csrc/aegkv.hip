@@ -84,6 +84,7 @@ struct Tunables {
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
   int64_t swap_unroll = 4;       // swap kernels: 16 B loads per lane (256-lane shape)
+  int64_t staged_workgroups = 0; // STAGED gather/scatter grid: 0 = one workgroup per item
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
@@ -746,7 +747,7 @@ struct Run {
 int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
                         const std::vector<int64_t>& order, size_t lo, size_t hi,
                         bool is_swap_in, bool staged, char* host_side, int64_t host_stride,
-                        int64_t host_rank_off, bool vec, hipStream_t stream) {
+                        int64_t host_rank_off, bool vec, int64_t wgs, hipStream_t stream) {
   const int32_t S = L.num_segments;
   const int64_t n = static_cast<int64_t>(hi - lo);
   if (n == 0) return 0;
@@ -804,7 +805,6 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   // Non-temporal stores only where the destination is HBM: plain stores to
   // the host pool measured faster (no L2 residency to avoid there).
   const bool nt = t.nt_stores != 0 && !(!is_swap_in && !staged);
-  const int64_t wgs = is_swap_in ? t.swap_in_workgroups : t.swap_out_workgroups;
   e = launch_swap(sh, !is_swap_in, vec, nt, launch_grid(wgs, items, sh.wg), stream, a);
   if (e != hipSuccess) {
     // the descriptor upload is already enqueued: retire its region in order
@@ -814,6 +814,9 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   }
   return ring_commit(ctx->ring, off, total, stream);
 }
+
+// A staged chunk with more host runs than this counts as scattered.
+constexpr size_t kManyRuns = 16;
 
 // Runs of host bytes one staged entry moves, merged when contiguous.
 void entry_runs(const SwapLayout& L, const SwapList& E, int64_t i, bool is_swap_in,
@@ -936,9 +939,12 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
 
   if (!staged) {
     std::lock_guard<std::mutex> lk(ctx->mu);
+    // link-bound: a few persistent workgroups
     return enqueue_swap_kernel(ctx, L, E, order, 0, order.size(), is_swap_in, false,
                                L.host_pool, L.host_page_bytes, L.host_rank_offset,
-                               dev_vec && host_vec, stream);
+                               dev_vec && host_vec,
+                               is_swap_in ? t.swap_in_workgroups : t.swap_out_workgroups,
+                               stream);
   }
 
   // STAGED: host-id order lets consecutive host pages merge into one DMA.
@@ -967,10 +973,17 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
         return rc;
       }
     }
+    // The gather/scatter moves HBM to HBM, so it gets a full grid, except a
+    // swap-out whose chunk leaves many host runs (scattered host ids, one
+    // page-sized copy each): there the copies measured faster behind the
+    // slower persistent grid (41.9 -> 50.1 GB/s), while a few large runs
+    // gain from the full grid (51.1 -> 55.3 GB/s).
+    const int64_t wgs = !is_swap_in && runs.size() > kManyRuns ? t.swap_out_workgroups
+                                                               : t.staged_workgroups;
     {
       std::lock_guard<std::mutex> lk(ctx->mu);
       rc = enqueue_swap_kernel(ctx, L, E, order, lo, hi, is_swap_in, true, st, composite, 0,
-                               vec_stage, stream);
+                               vec_stage, wgs, stream);
     }
     if (rc) {
       (void)hipFreeAsync(staging, stream);
@@ -1130,6 +1143,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
     case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
     case AEGKV_TUNE_SWAP_UNROLL: slot = &g_tune.swap_unroll; break;
+    case AEGKV_TUNE_STAGED_WORKGROUPS: slot = &g_tune.staged_workgroups; break;
     case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
     case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
@@ -1146,6 +1160,8 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "staging must be at least 1 MiB");
     if (key == AEGKV_TUNE_COPY_WGS_PER_CU && value > 64)
       return fail(AEGKV_EINVAL, "copy workgroups per CU must be in [0, 64]");
+    if (key == AEGKV_TUNE_STAGED_WORKGROUPS && value > (int64_t(1) << 24))
+      return fail(AEGKV_EINVAL, "staged workgroups must be in [0, 2^24]");
     if (key == AEGKV_TUNE_SWAP_UNROLL && value != 1 && value != 2 && value != 4)
       return fail(AEGKV_EINVAL, "swap unroll must be 1, 2 or 4");
     if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && !valid_copy_unroll(value))

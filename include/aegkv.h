@@ -82,6 +82,8 @@ extern "C" {
                                         workgroups per CU; default 96 KiB) */
 #define AEGKV_TUNE_SWAP_UNROLL 12    /* swap kernels: 16 B loads per lane of
                                         the 256-lane shape (1, 2 or 4)      */
+#define AEGKV_TUNE_STAGED_WORKGROUPS 13 /* STAGED gather/scatter grid (0 = one
+                                           workgroup per item)             */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

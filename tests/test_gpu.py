@@ -285,7 +285,7 @@ def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
             _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
-            _lib.TUNE_SWAP_UNROLL)
+            _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -366,6 +366,7 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     staging chunks) land exactly where the oracle puts them, both ways."""
     _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, dma_streams)
     _lib.tune(_lib.TUNE_STAGING_BYTES, 1 << 20)
+    _lib.tune(_lib.TUNE_STAGED_WORKGROUPS, (0, 3, 64, 1)[dma_streams % 4])
     rng = np.random.default_rng(50 + dma_streams)
     page = np.array([64 * 1024, 16 * 1024, 48 * 1024], np.int64)
     cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)

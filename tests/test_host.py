@@ -285,6 +285,9 @@ def test_tuning_knobs(aegkv_lib):
         _lib.tune(99, 1)
     assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
     assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 4
+    assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_STAGED_WORKGROUPS, 1 << 25)
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_UNROLL, 3)
     with pytest.raises(ValueError):
