@@ -86,6 +86,14 @@ struct Tunables {
   int64_t swap_unroll = 4;       // swap kernels: 16 B loads per lane (256-lane shape)
   int64_t staged_workgroups = 0; // STAGED gather/scatter grid: 0 = one workgroup per item
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
+  // STAGED over library streams: two staging chunks in flight (bit 0
+  // swap-out, bit 1 swap-in). Swap-in gains either way (54.0 -> 55.3 GB/s
+  // scattered, 55.1 -> 56.4 contiguous). Swap-out gains (50.3 -> 54.3) only
+  // while the runtime runs its device-to-host copies as shader blits; when
+  // the host enqueues ahead of a busy GPU the runtime moved them to SDMA
+  // engines, where the overlapped swap-out fell to 24 GB/s against 33-40
+  // one chunk at a time, so swap-out stays serial by default.
+  int64_t staged_overlap = 2;
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
   // 32-160 KiB tiles; 16 KiB items lose 14 % at one per CU, so they keep 0).
@@ -346,12 +354,15 @@ struct DeviceCtx {
   // directions share the set: separate sets per direction add streams that
   // share the process's 4 hardware queues with the callers' streams, and
   // measured slower (one direction alone 50.0 -> 45.4-47.6 GB/s).
+  // A staged call holds the set's mutex from its first fork to its last
+  // join, so its events are not re-recorded by another call in between.
   struct DmaSet {
     std::mutex mu;
     int streams = 0;
     hipStream_t st[kMaxDmaStreams] = {};
     hipEvent_t fork_ev = nullptr;
-    hipEvent_t join_ev[kMaxDmaStreams] = {};
+    hipEvent_t join_ev[2][kMaxDmaStreams] = {};  // copies done, per staging buffer
+    hipEvent_t kernel_ev[2] = {};                // gather / scatter done, per staging buffer
   } dma;
 };
 
@@ -863,32 +874,72 @@ hipError_t dedicated_stream(hipStream_t* out) {
 
 // Create the DMA streams and events once (caller holds the set's mutex).
 int ensure_dma(DeviceCtx::DmaSet& d, int k) {
-  if (!d.fork_ev) AEGKV_HIP(hipEventCreateWithFlags(&d.fork_ev, hipEventDisableTiming));
+  if (!d.fork_ev) {
+    AEGKV_HIP(hipEventCreateWithFlags(&d.kernel_ev[0], hipEventDisableTiming));
+    AEGKV_HIP(hipEventCreateWithFlags(&d.kernel_ev[1], hipEventDisableTiming));
+    AEGKV_HIP(hipEventCreateWithFlags(&d.fork_ev, hipEventDisableTiming));
+  }
   while (d.streams < k) {
     const int i = d.streams;
     AEGKV_HIP(hipStreamCreateWithFlags(&d.st[i], hipStreamNonBlocking));
-    AEGKV_HIP(hipEventCreateWithFlags(&d.join_ev[i], hipEventDisableTiming));
+    AEGKV_HIP(hipEventCreateWithFlags(&d.join_ev[0][i], hipEventDisableTiming));
+    AEGKV_HIP(hipEventCreateWithFlags(&d.join_ev[1][i], hipEventDisableTiming));
     ++d.streams;
   }
   return 0;
 }
 
-// Copy the staged runs between staging and the host pool. With k > 1 the
-// copies fan out over the context's DMA streams, balanced by bytes (fork
-// after everything the caller's stream holds, join before anything it
-// enqueues next), which overlaps the runtime's per-copy gaps.
-int issue_runs(DeviceCtx* ctx, const std::vector<Run>& runs, bool to_device, char* staging,
-               char* host, hipStream_t caller, int k) {
-  const hipMemcpyKind kind = to_device ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
-  auto copy = [&](const Run& r, hipStream_t st) -> hipError_t {
-    char* s_ptr = staging + r.stage_off;
-    char* h_ptr = host + r.host_off;
-    return to_device ? hipMemcpyAsync(s_ptr, h_ptr, static_cast<size_t>(r.len), kind, st)
-                     : hipMemcpyAsync(h_ptr, s_ptr, static_cast<size_t>(r.len), kind, st);
-  };
+hipError_t copy_run(const Run& r, bool to_device, char* staging, char* host, hipStream_t st) {
+  char* s_ptr = staging + r.stage_off;
+  char* h_ptr = host + r.host_off;
+  const size_t len = static_cast<size_t>(r.len);
+  return to_device ? hipMemcpyAsync(s_ptr, h_ptr, len, hipMemcpyHostToDevice, st)
+                   : hipMemcpyAsync(h_ptr, s_ptr, len, hipMemcpyDeviceToHost, st);
+}
+
+// Copy the staged runs of one chunk between staging and the host pool over
+// the k DMA streams, balanced by bytes, and record join[i] behind stream i's
+// share (caller holds the set's mutex).
+int runs_on_dma(DeviceCtx::DmaSet& d, int k, const std::vector<Run>& runs, bool to_device,
+                char* staging, char* host, hipEvent_t* join) {
+  int64_t load[kMaxDmaStreams] = {};
+  for (const Run& r : runs) {
+    const int i = static_cast<int>(std::min_element(load, load + k) - load);
+    load[i] += r.len;
+    hipError_t e = copy_run(r, to_device, staging, host, d.st[i]);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staged run)");
+  }
+  for (int i = 0; i < k; ++i) AEGKV_HIP(hipEventRecord(join[i], d.st[i]));
+  return 0;
+}
+
+// The gather (swap-out) or scatter (swap-in) kernel of staged chunk
+// order[lo, hi) whose host side is `staging` (one composite page per entry).
+// It moves HBM to HBM, so it gets a full grid, except a swap-out whose chunk
+// leaves many host runs (scattered host ids, one page-sized copy each):
+// there the copies measured faster beside the slower persistent grid
+// (41.9 -> 50.1 GB/s), while a few large runs gain from the full grid
+// (51.1 -> 55.3 GB/s).
+int staged_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
+                  const std::vector<int64_t>& order, size_t lo, size_t hi, bool is_swap_in,
+                  char* staging, int64_t composite, bool vec_stage, size_t num_runs,
+                  const Tunables& t, hipStream_t stream) {
+  const int64_t wgs = !is_swap_in && num_runs > kManyRuns ? t.swap_out_workgroups
+                                                          : t.staged_workgroups;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return enqueue_swap_kernel(ctx, L, E, order, lo, hi, is_swap_in, true, staging, composite, 0,
+                             vec_stage, wgs, stream);
+}
+
+// Copy one chunk's runs between staging and the host pool and return the
+// caller's stream to after them: on the caller's stream itself (k <= 1), or
+// forked over the k DMA streams (after everything the caller's stream
+// holds) and joined back, which overlaps the runtime's per-copy gaps.
+int chunk_copies(DeviceCtx* ctx, int k, const std::vector<Run>& runs, bool to_device,
+                 char* staging, char* host, hipStream_t stream) {
   if (k <= 1) {
     for (const Run& r : runs) {
-      hipError_t e = copy(r, caller);
+      hipError_t e = copy_run(r, to_device, staging, host, stream);
       if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staged run)");
     }
     return 0;
@@ -897,19 +948,142 @@ int issue_runs(DeviceCtx* ctx, const std::vector<Run>& runs, bool to_device, cha
   std::lock_guard<std::mutex> lk(d.mu);
   int rc = ensure_dma(d, k);
   if (rc) return rc;
-  AEGKV_HIP(hipEventRecord(d.fork_ev, caller));
-  for (int i = 0; i < k; ++i) AEGKV_HIP(hipStreamWaitEvent(d.st[i], d.fork_ev, 0));
-  std::vector<int64_t> load(static_cast<size_t>(k), 0);
-  for (const Run& r : runs) {
-    const int i = static_cast<int>(std::min_element(load.begin(), load.end()) - load.begin());
-    load[static_cast<size_t>(i)] += r.len;
-    hipError_t e = copy(r, d.st[i]);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(staged run)");
+  AEGKV_HIP(hipEventRecord(d.fork_ev, stream));
+  for (int j = 0; j < k; ++j) AEGKV_HIP(hipStreamWaitEvent(d.st[j], d.fork_ev, 0));
+  rc = runs_on_dma(d, k, runs, to_device, staging, host, d.join_ev[0]);
+  // join whatever was enqueued, also after a failed copy
+  for (int j = 0; j < k; ++j) {
+    if (rc && hipEventRecord(d.join_ev[0][j], d.st[j]) != hipSuccess) continue;
+    hipError_t e = hipStreamWaitEvent(stream, d.join_ev[0][j], 0);
+    if (e != hipSuccess && !rc) rc = hip_fail(e, "hipStreamWaitEvent(staged copies)");
   }
-  for (int i = 0; i < k; ++i) {
-    AEGKV_HIP(hipEventRecord(d.join_ev[i], d.st[i]));
-    AEGKV_HIP(hipStreamWaitEvent(caller, d.join_ev[i], 0));
+  return rc;
+}
+
+// STAGED one chunk after another, each through its own stream-ordered
+// staging allocation: swap-out gathers a chunk and then copies it to the
+// host, swap-in copies a chunk from the host and then scatters it.
+int staged_serial(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
+                  const std::vector<int64_t>& order, bool is_swap_in, int64_t composite,
+                  size_t step, bool vec_stage, const Tunables& t, int k, hipStream_t stream) {
+  std::vector<Run> runs;
+  for (size_t lo = 0; lo < order.size(); lo += step) {
+    const size_t hi = std::min(order.size(), lo + step);
+    runs.clear();
+    for (size_t j = lo; j < hi; ++j)
+      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
+    void* p = nullptr;
+    AEGKV_HIP(hipMallocAsync(&p, (hi - lo) * static_cast<size_t>(composite), stream));
+    char* buf = static_cast<char*>(p);
+    int rc = 0;
+    if (is_swap_in) rc = chunk_copies(ctx, k, runs, true, buf, L.host_pool, stream);
+    if (!rc)
+      rc = staged_kernel(ctx, L, E, order, lo, hi, is_swap_in, buf, composite, vec_stage,
+                         runs.size(), t, stream);
+    if (!rc && !is_swap_in) rc = chunk_copies(ctx, k, runs, false, buf, L.host_pool, stream);
+    if (rc) {
+      (void)hipFreeAsync(buf, stream);
+      return rc;
+    }
+    AEGKV_HIP(hipFreeAsync(buf, stream));
   }
+  return 0;
+}
+
+// STAGED with the copies on the library's k DMA streams and two staging
+// buffers, so the gather (swap-out) or scatter (swap-in) of one chunk runs
+// while another chunk's copies use the link. Chunk c uses buffer b = c % 2:
+//   swap-out: the caller's stream waits the copies of chunk c-2 and gathers
+//             chunk c into buffer b; the DMA streams wait that gather, copy
+//             the chunk to the host and record join_ev[b];
+//   swap-in:  the DMA streams wait the scatter of chunk c-2, copy chunk c
+//             from the host into buffer b and record join_ev[b]; the
+//             caller's stream waits those and scatters the chunk.
+// The DMA streams start after everything the caller's stream holds, the
+// staging allocations included; the caller's stream ends after every copy
+// and frees the buffers there.
+int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
+                      const std::vector<int64_t>& order, bool is_swap_in, int64_t composite,
+                      size_t step, bool vec_stage, const Tunables& t, int k,
+                      hipStream_t stream) {
+  DeviceCtx::DmaSet& d = ctx->dma;
+  std::lock_guard<std::mutex> lk(d.mu);
+  int rc = ensure_dma(d, k);
+  if (rc) return rc;
+  const size_t n = order.size();
+  const size_t chunks = (n + step - 1) / step;
+  const int nbuf = chunks > 1 ? 2 : 1;
+  const size_t buf_bytes = std::min(step, n) * static_cast<size_t>(composite);
+  char* buf[2] = {nullptr, nullptr};
+  for (int b = 0; b < nbuf; ++b) {
+    void* p = nullptr;
+    hipError_t e = hipMallocAsync(&p, buf_bytes, stream);
+    if (e != hipSuccess) {
+      if (b) (void)hipFreeAsync(buf[0], stream);
+      return hip_fail(e, "hipMallocAsync(staging)");
+    }
+    buf[b] = static_cast<char*>(p);
+  }
+  // On a failure after work was enqueued: join every DMA stream back into
+  // the caller's stream and free the buffers behind it.
+  auto unwind = [&](int status) {
+    for (int j = 0; j < k; ++j)
+      if (hipEventRecord(d.join_ev[0][j], d.st[j]) == hipSuccess)
+        (void)hipStreamWaitEvent(stream, d.join_ev[0][j], 0);
+    for (int b = 0; b < nbuf; ++b) (void)hipFreeAsync(buf[b], stream);
+    (void)hipGetLastError();
+    return status;
+  };
+  // every DMA stream waits `ev`, recorded on `on`
+  auto fan_in = [&](hipEvent_t ev, hipStream_t on) {
+    hipError_t e = hipEventRecord(ev, on);
+    for (int j = 0; j < k && e == hipSuccess; ++j) e = hipStreamWaitEvent(d.st[j], ev, 0);
+    return e;
+  };
+  // the caller's stream waits the copies that recorded join_ev[b]
+  auto join = [&](int b) {
+    hipError_t e = hipSuccess;
+    for (int j = 0; j < k && e == hipSuccess; ++j) e = hipStreamWaitEvent(stream, d.join_ev[b][j], 0);
+    return e;
+  };
+  hipError_t e = fan_in(d.fork_ev, stream);
+  if (e != hipSuccess) return unwind(hip_fail(e, "staged fork"));
+  std::vector<Run> runs;
+  for (size_t c = 0; c < chunks; ++c) {
+    const size_t lo = c * step, hi = std::min(n, lo + step);
+    const int b = static_cast<int>(c & 1);
+    runs.clear();
+    for (size_t j = lo; j < hi; ++j)
+      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
+    if (!is_swap_in) {
+      if (c >= 2 && (e = join(b)) != hipSuccess)
+        return unwind(hip_fail(e, "hipStreamWaitEvent(staged copies)"));
+      rc = staged_kernel(ctx, L, E, order, lo, hi, false, buf[b], composite, vec_stage,
+                         runs.size(), t, stream);
+      if (rc) return unwind(rc);
+      if ((e = fan_in(d.kernel_ev[b], stream)) != hipSuccess)
+        return unwind(hip_fail(e, "staged gather event"));
+      rc = runs_on_dma(d, k, runs, false, buf[b], L.host_pool, d.join_ev[b]);
+      if (rc) return unwind(rc);
+    } else {
+      for (int j = 0; c >= 2 && j < k && e == hipSuccess; ++j)
+        e = hipStreamWaitEvent(d.st[j], d.kernel_ev[b], 0);
+      if (e != hipSuccess) return unwind(hip_fail(e, "hipStreamWaitEvent(staged scatter)"));
+      rc = runs_on_dma(d, k, runs, true, buf[b], L.host_pool, d.join_ev[b]);
+      if (rc) return unwind(rc);
+      if ((e = join(b)) != hipSuccess)
+        return unwind(hip_fail(e, "hipStreamWaitEvent(staged copies)"));
+      rc = staged_kernel(ctx, L, E, order, lo, hi, true, buf[b], composite, vec_stage,
+                         runs.size(), t, stream);
+      if (rc) return unwind(rc);
+      if ((e = hipEventRecord(d.kernel_ev[b], stream)) != hipSuccess)
+        return unwind(hip_fail(e, "staged scatter event"));
+    }
+  }
+  // swap-out: each DMA stream's last join follows all of its earlier copies
+  if (!is_swap_in && (e = join(static_cast<int>((chunks - 1) & 1))) != hipSuccess)
+    return unwind(hip_fail(e, "hipStreamWaitEvent(staged copies)"));
+  for (int b = 0; b < nbuf; ++b) AEGKV_HIP(hipFreeAsync(buf[b], stream));
   return 0;
 }
 
@@ -951,54 +1125,17 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   const int64_t* host_ids = is_swap_in ? E.src : E.dst;
   std::stable_sort(order.begin(), order.end(),
                    [&](int64_t a, int64_t b) { return host_ids[a] < host_ids[b]; });
-  const int64_t per_chunk =
-      std::max<int64_t>(1, std::min<int64_t>(E.n, t.staging_bytes / composite));
+  const size_t step = static_cast<size_t>(
+      std::max<int64_t>(1, std::min<int64_t>(E.n, t.staging_bytes / composite)));
   // Staging comes from hipMallocAsync (256 B aligned) with a composite stride.
   const bool vec_stage = dev_vec && composite % 16 == 0;
-  std::vector<Run> runs;
-  for (size_t lo = 0; lo < order.size(); lo += static_cast<size_t>(per_chunk)) {
-    const size_t hi = std::min(order.size(), lo + static_cast<size_t>(per_chunk));
-    const int64_t m = static_cast<int64_t>(hi - lo);
-    runs.clear();
-    for (size_t j = lo; j < hi; ++j)
-      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
-    void* staging = nullptr;
-    AEGKV_HIP(hipMallocAsync(&staging, static_cast<size_t>(m * composite), stream));
-    char* st = static_cast<char*>(staging);
-    const int k = static_cast<int>(std::min<int64_t>(t.staged_dma_streams, kMaxDmaStreams));
-    if (is_swap_in) {
-      rc = issue_runs(ctx, runs, true, st, L.host_pool, stream, k);
-      if (rc) {
-        (void)hipFreeAsync(staging, stream);
-        return rc;
-      }
-    }
-    // The gather/scatter moves HBM to HBM, so it gets a full grid, except a
-    // swap-out whose chunk leaves many host runs (scattered host ids, one
-    // page-sized copy each): there the copies measured faster behind the
-    // slower persistent grid (41.9 -> 50.1 GB/s), while a few large runs
-    // gain from the full grid (51.1 -> 55.3 GB/s).
-    const int64_t wgs = !is_swap_in && runs.size() > kManyRuns ? t.swap_out_workgroups
-                                                               : t.staged_workgroups;
-    {
-      std::lock_guard<std::mutex> lk(ctx->mu);
-      rc = enqueue_swap_kernel(ctx, L, E, order, lo, hi, is_swap_in, true, st, composite, 0,
-                               vec_stage, wgs, stream);
-    }
-    if (rc) {
-      (void)hipFreeAsync(staging, stream);
-      return rc;
-    }
-    if (!is_swap_in) {
-      rc = issue_runs(ctx, runs, false, st, L.host_pool, stream, k);
-      if (rc) {
-        (void)hipFreeAsync(staging, stream);
-        return rc;
-      }
-    }
-    AEGKV_HIP(hipFreeAsync(staging, stream));
-  }
-  return 0;
+  const int k = static_cast<int>(std::min<int64_t>(t.staged_dma_streams, kMaxDmaStreams));
+  const bool overlap = (t.staged_overlap >> (is_swap_in ? 1 : 0)) & 1;
+  if (k <= 1 || !overlap)
+    return staged_serial(ctx, L, E, order, is_swap_in, composite, step, vec_stage, t, k,
+                         stream);
+  return staged_overlapped(ctx, L, E, order, is_swap_in, composite, step, vec_stage, t, k,
+                           stream);
 }
 
 // Whole-block copies from a source cache to a target cache (the same cache
@@ -1146,6 +1283,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_STAGED_WORKGROUPS: slot = &g_tune.staged_workgroups; break;
     case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
     case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
+    case AEGKV_TUNE_STAGED_OVERLAP: slot = &g_tune.staged_overlap; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -1173,6 +1311,8 @@ int64_t aegkv_tune(int key, int64_t value) {
                   static_cast<long long>(kMaxLdsPerWorkgroup));
     if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
+    if (key == AEGKV_TUNE_STAGED_OVERLAP && value > 3)
+      return fail(AEGKV_EINVAL, "staged overlap is a 2-bit mask (0-3)");
     *slot = value;
   }
   return prev;

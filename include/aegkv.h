@@ -84,6 +84,10 @@ extern "C" {
                                         the 256-lane shape (1, 2 or 4)      */
 #define AEGKV_TUNE_STAGED_WORKGROUPS 13 /* STAGED gather/scatter grid (0 = one
                                            workgroup per item)             */
+#define AEGKV_TUNE_STAGED_OVERLAP 14 /* STAGED over library streams: two
+                                        staging chunks in flight, bit 0 for
+                                        swap-out, bit 1 for swap-in
+                                        (default 2)                        */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -285,7 +285,7 @@ def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
             _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
-            _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS)
+            _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS, _lib.TUNE_STAGED_OVERLAP)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -400,6 +400,47 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     torch.cuda.synchronize()
     for s in range(3):
         assert np.array_equal(segs[s].cpu().numpy(), want_segs[s]), s
+    pool.free()
+
+
+@pytest.mark.parametrize("dma_streams,contiguous,overlap",
+                         [(2, True, 3), (2, False, 3), (4, False, 3), (2, False, 0),
+                          (1, True, 3)])
+def test_staged_chunked_round_trip(gpu, restore_tuning, dma_streams, contiguous, overlap):
+    """STAGED over library streams with two staging buffers in flight (the
+    gather or scatter of one chunk beside the copies of another), one chunk
+    at a time, and on the caller's stream; with 8 MiB chunks of 3 Qwen3-4B
+    pages, 200 blocks pass through 67 chunks each way, so each buffer is
+    reused many times. Host pages must equal the device tiles they came
+    from and the round trip must be exact."""
+    _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, dma_streams)
+    _lib.tune(_lib.TUNE_STAGING_BYTES, 8 << 20)
+    _lib.tune(_lib.TUNE_STAGED_OVERLAP, overlap)
+    _say("STAGED chunks", dma_streams, "contiguous" if contiguous else "scattered", overlap)
+    segs = _kv_segments(36, 512, 8, 128, torch.bfloat16, gpu, 11)
+    tile = 16 * 8 * 128 * 2
+    S, n = len(segs), 200
+    pool = ops.PinnedHostPool(512 * S * tile)
+    g = torch.Generator().manual_seed(12 + dma_streams)
+    perm = torch.randperm(512, generator=g).numpy()
+    out_ids, in_ids = perm[:n], perm[n:2 * n]
+    host_ids = (np.arange(100, 100 + n) if contiguous
+                else torch.randperm(512, generator=g)[:n].numpy())
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, 512, [1], pool.tensor,
+              S * tile, 0)
+    z = np.zeros(n, np.int32)
+    ops.swap_segments(segs, *common, out_ids, host_ids, z, z, z + 1, False, mode="staged")
+    torch.cuda.synchronize()
+    dev_out = torch.from_numpy(out_ids).to(gpu)
+    want = torch.stack([s_.view(512, -1).view(torch.uint8)[dev_out] for s_ in segs], dim=1)
+    pages = pool.tensor.view(512, S, tile)[torch.from_numpy(host_ids)].to(gpu)
+    assert torch.equal(pages, want)
+    del pages, want
+    ops.swap_segments(segs, *common, host_ids, in_ids, z, z, z + 1, True, mode="staged")
+    torch.cuda.synchronize()
+    dev_in = torch.from_numpy(in_ids).to(gpu)
+    for s in range(S):
+        assert torch.equal(segs[s][dev_in], segs[s][dev_out]), s
     pool.free()
 
 

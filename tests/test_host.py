@@ -286,6 +286,9 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
     assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 4
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
+    assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 2
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_STAGED_OVERLAP, 4)
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_STAGED_WORKGROUPS, 1 << 25)
     with pytest.raises(ValueError):
