@@ -10,16 +10,18 @@
 // lanes moves CHUNK = 256 * 16 * UNROLL bytes per item with all UNROLL loads
 // issued before the first store. Items are entry-major so consecutive items
 // walk one composite host page in address order (good for PCIe write
-// combining and host DRAM pages); the grid is a fixed number of workgroups
-// per CU that stride over the item space.
+// combining and host DRAM pages); link-bound swaps run a few persistent
+// workgroups that stride over the item space, HBM-bound moves one workgroup
+// per item.
 //
 // Two host-transfer designs share the kernel:
 //   DIRECT: the "host side" pointer is the pinned host pool itself (mapped
 //           into the GPU address space by hipHostMalloc); the kernel's
 //           loads/stores cross PCIe.
 //   STAGED: the "host side" pointer is a contiguous device staging buffer
-//           laid out like the host pages; SDMA hipMemcpyAsync moves merged
-//           runs between staging and the host pool.
+//           laid out like the host pages; hipMemcpyAsync moves merged runs
+//           between staging and the host pool (the runtime runs each copy
+//           as a blit kernel or on an SDMA engine).
 //
 // Entry-point contracts are in include/aegkv.h.
 
