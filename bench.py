@@ -14,7 +14,10 @@ Every operation is one libaegkv call on the current stream, timed with HIP
 events recorded on that stream. Other configs (--config): varlen, overlap,
 refplan, switch (see --help). `value` is the swap throughput (both
 directions' bytes over their summed time); the copy_blocks kernel carries
-the HBM roofline, the swaps the measured-host-link roofline.
+the HBM roofline, the swaps the measured-host-link roofline. The line also
+reports the two host-transfer designs (DIRECT, STAGED) side by side on the
+same blocks, one call at a time, the reference's per-extent copy loop on the
+same GPU, and a model switch (both link directions at once).
 
 The CPU baseline times the reference's torch path (one narrow().copy_() per
 (segment, block) extent, aegaeon/worker.py:2272-2328) on host tensors of the
@@ -54,6 +57,8 @@ def parse():
     p.add_argument("--no-switch", action="store_true",
                    help="skip the model-switch line (both link directions at once)")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--no-side-by-side", action="store_true",
+                   help="skip the DIRECT vs STAGED side-by-side measurement")
     p.add_argument("--no-reference-loop", action="store_true",
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
@@ -923,6 +928,32 @@ def main():
             "speedup_d2h": round(d2h_gbps / ref["d2h"], 2),
             "speedup_h2d": round(h2d_gbps / ref["h2d"], 2),
         }
+    # The two host-transfer designs side by side on the same blocks, one
+    # call at a time (each call timed alone, GPU idle when it is enqueued).
+    line["designs_side_by_side"] = None
+    if not args.no_side_by_side:
+        log("DIRECT and STAGED side by side, one call at a time")
+        side = {}
+        for mode in ("direct", "staged"):
+            rates = {"d2h": [], "h2d": []}
+            for rep in range(4):
+                for name, sargs in (("d2h", (out_ids, host_ids, zero, zero, ones, False)),
+                                    ("h2d", (host_ids, in_ids, zero, zero, ones, True))):
+                    torch.cuda.synchronize()
+                    a, b = ev_pair(torch)
+                    a.record()
+                    lay.swap(*sargs, mode=mode)
+                    b.record()
+                    b.synchronize()
+                    if rep:
+                        rates[name].append(swap_bytes / (a.elapsed_time(b) / 1e3) / 1e9)
+            if not all(torch.equal(s[di], s[do]) for s in segs1):
+                raise AssertionError(f"{mode} side-by-side round trip is not bit-exact")
+            side[mode] = {k: round(float(np.median(v)), 3) for k, v in rates.items()}
+        line["designs_side_by_side"] = {
+            "what": "same 1024 blocks and pool; median of 3 calls per direction after one "
+                    "warm-up, each call timed alone",
+            "direct_GBps": side["direct"], "staged_GBps": side["staged"]}
     pool.free()
     del segs1, segs2
     torch.cuda.empty_cache()
