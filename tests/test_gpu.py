@@ -280,6 +280,58 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
     assert np.array_equal(seg.cpu().numpy(), segs_np[4])
 
 
+@pytest.mark.parametrize("case", range(24))
+def test_randomized_block_copies_vs_oracle(gpu, oracle, restore_tuning, case):
+    """Random copy_blocks within one cache (1-20 segments of 16 B-multiple
+    or odd pages, repeated sources, random kernel shapes, grids, LDS
+    reservations and store kinds) against the oracle; every third case a
+    migrate_blocks between two caches of different block counts against
+    the closed form dst[d] = src[s]."""
+    rng = np.random.default_rng(7000 + case)
+    _lib.tune(_lib.TUNE_COPY_UNROLL, int(rng.choice([0, 0, 1, 2, 3, 4, 5, 6, 8, 10])))
+    _lib.tune(_lib.TUNE_COPY_WGS_PER_CU, int(rng.choice([0, 0, 1, 4])))
+    _lib.tune(_lib.TUNE_COPY_LDS_BYTES, int(rng.choice([0, 96 << 10])))
+    _lib.tune(_lib.TUNE_NT_STORES, int(rng.integers(0, 2)))
+    n_seg = int(rng.integers(1, 21))
+    if rng.random() < 0.2:
+        page = rng.choice([5, 48, 100, 4096 + 3], n_seg)           # byte path
+    else:
+        page = rng.choice([16, 256, 4096, 16384, 32768, 48 * 1024 + 16, 160 * 1024], n_seg)
+    page = page.astype(np.int64)
+    n_src = int(rng.integers(2, 81))
+    migrate = case % 3 == 2
+    n_dst = int(rng.integers(2, 81)) if migrate else n_src
+    _say("randomized block copies", case, "migrate" if migrate else "copy_blocks", "segments",
+         n_seg, "blocks", n_src, n_dst)
+    src_np = [rng.integers(0, 256, (n_src, int(p)), dtype=np.uint8) for p in page]
+    if migrate:
+        n = int(rng.integers(0, n_dst + 1))
+        dst_ids = rng.permutation(n_dst)[:n]
+        src_ids = rng.integers(0, n_src, n)
+        dst_np = [rng.integers(0, 256, (n_dst, int(p)), dtype=np.uint8) for p in page]
+        src_t = [torch.from_numpy(x.copy()).to(gpu) for x in src_np]
+        dst_t = [torch.from_numpy(x.copy()).to(gpu) for x in dst_np]
+        ops.migrate_blocks(src_t, dst_t, src_ids, dst_ids)
+        for x, y in zip(src_np, dst_np):
+            y[dst_ids] = x[src_ids]
+        torch.cuda.synchronize()
+        for i in range(n_seg):
+            assert np.array_equal(dst_t[i].cpu().numpy(), dst_np[i]), i
+            assert np.array_equal(src_t[i].cpu().numpy(), src_np[i]), i
+        return
+    perm = rng.permutation(n_src)
+    n = int(rng.integers(0, n_src // 2 + 1))
+    dst_ids = perm[:n]
+    pool = perm[n:]
+    src_ids = pool[rng.integers(0, pool.size, n)] if n else perm[:0]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in src_np]
+    ops.copy_blocks(segs, src_ids, dst_ids)
+    oracle.copy_blocks([x.reshape(-1) for x in src_np], page, n_src, src_ids, dst_ids)
+    torch.cuda.synchronize()
+    for i in range(n_seg):
+        assert np.array_equal(segs[i].cpu().numpy(), src_np[i]), i
+
+
 @pytest.fixture
 def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
@@ -442,6 +494,82 @@ def test_staged_chunked_round_trip(gpu, restore_tuning, dma_streams, contiguous,
     for s in range(S):
         assert torch.equal(segs[s][dev_in], segs[s][dev_out]), s
     pool.free()
+
+
+def _random_case(rng):
+    """A random composite layout, host pool geometry and swap list: 1-4
+    cache groups with 1-17 kernel blocks per page, 1-24 segments owned by
+    random group sets, 16 B-multiple or odd tile units, TP 1-3."""
+    n_groups = int(rng.integers(1, 5))
+    kpp = rng.choice([1, 2, 4, 8, 17], n_groups).astype(np.int64)
+    n_seg = int(rng.integers(1, 25))
+    owners = rng.integers(1, 1 << n_groups, n_seg).astype(np.uint64)
+    byte_path = rng.random() < 0.25
+    page = []
+    for o in owners:
+        lcm = 1
+        for g in range(n_groups):
+            if (int(o) >> g) & 1:
+                lcm = int(np.lcm(lcm, int(kpp[g])))
+        unit = int(rng.choice([3, 7, 5])) if byte_path else int(rng.choice([16, 32, 64, 1024, 4096]))
+        page.append(lcm * unit)
+    page = np.array(page, np.int64)
+    cpu_off = np.concatenate([[0], np.cumsum(page)[:-1]]).astype(np.int64)
+    tp_size = int(rng.integers(1, 4))
+    n_gpu, n_host = int(rng.integers(1, 41)), int(rng.integers(1, 41))
+    n = int(rng.integers(0, min(n_gpu, n_host) + 1))
+    grp = rng.integers(0, n_groups, n).astype(np.int32)
+    first = np.array([rng.integers(0, kpp[g] + 1) for g in grp], np.int64)
+    valid = np.array([rng.integers(0, kpp[g] - f + 1) for g, f in zip(grp, first)], np.int64)
+    return dict(kpp=kpp, page=page, owners=owners, cpu_off=cpu_off, tp_size=tp_size,
+                tp_rank=int(rng.integers(0, tp_size)), n_gpu=n_gpu, n_host=n_host, n=n,
+                grp=grp, first=first, valid=valid)
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
+    """Random layouts (groups, extents, TP ranks, byte and 16 B paths),
+    both modes, random staging chunk sizes, DMA stream counts, overlap
+    settings and host-pool alignments: swap-out then swap-in to other ids,
+    each byte-equal to the oracle."""
+    rng = np.random.default_rng(9000 + case)
+    c = _random_case(rng)
+    mode = MODES[case % 2]
+    _lib.tune(_lib.TUNE_STAGING_BYTES, int(rng.choice([1 << 20, 3 << 20, 512 << 20])))
+    _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, int(rng.choice([0, 1, 2, 4])))
+    _lib.tune(_lib.TUNE_STAGED_OVERLAP, int(rng.integers(0, 4)))
+    shift = int(rng.choice([0, 0, 16, 1]))
+    page, kpp, n = c["page"], c["kpp"], c["n"]
+    composite = int(page.sum())
+    host_page = composite * c["tp_size"]
+    _say("randomized swap", case, mode, "segments", len(page), "groups", len(kpp), "entries", n,
+         "tp", c["tp_size"], "host shift", shift)
+    segs_np = [rng.integers(0, 256, (c["n_gpu"], int(p)), dtype=np.uint8) for p in page]
+    host_np = rng.integers(0, 256, (c["n_host"], host_page), dtype=np.uint8)
+    raw = ops.PinnedHostPool(host_np.size + shift)
+    host = raw.tensor.narrow(0, shift, host_np.size)
+    host.copy_(torch.from_numpy(host_np.reshape(-1)))
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    src = rng.permutation(c["n_gpu"])[:n]
+    dst = rng.permutation(c["n_host"])[:n]
+    common = (page, c["cpu_off"], c["owners"], c["n_gpu"], kpp, host, host_page,
+              c["tp_rank"] * composite)
+    ops.swap_segments(segs, *common, src, dst, c["grp"], c["first"], c["valid"], False,
+                      mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, c["cpu_off"], c["owners"],
+                       c["n_gpu"], kpp, host_np.reshape(-1), host_page, c["tp_rank"], composite,
+                       src, dst, c["grp"], c["first"], c["valid"], False)
+    back = rng.permutation(c["n_gpu"])[:n]
+    ops.swap_segments(segs, *common, dst, back, c["grp"], c["first"], c["valid"], True,
+                      mode=mode)
+    oracle.swap_blocks([x.reshape(-1) for x in segs_np], page, c["cpu_off"], c["owners"],
+                       c["n_gpu"], kpp, host_np.reshape(-1), host_page, c["tp_rank"], composite,
+                       dst, back, c["grp"], c["first"], c["valid"], True)
+    torch.cuda.synchronize()
+    assert np.array_equal(host.numpy().reshape(host_np.shape), host_np)
+    for i in range(len(page)):
+        assert np.array_equal(segs[i].cpu().numpy(), segs_np[i]), i
+    raw.free()
 
 
 # ------------------------------------------------------- uncached host pool --
