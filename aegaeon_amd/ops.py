@@ -37,17 +37,26 @@ def _mode(mode) -> int:
     return int(mode)
 
 
-def _i64(values) -> np.ndarray:
+def _ints(values) -> np.ndarray:
+    """A flat integer array; floats and booleans are refused rather than
+    truncated (an empty list is fine)."""
     if isinstance(values, torch.Tensor):
         values = values.detach().cpu().numpy()
-    a = np.ascontiguousarray(np.asarray(values, dtype=np.int64).reshape(-1))
+    a = np.asarray(values).reshape(-1)
+    if a.size and a.dtype.kind not in "iu":
+        raise ValueError(f"expected integers, got {a.dtype} values")
     return a
 
 
+def _i64(values) -> np.ndarray:
+    return np.ascontiguousarray(_ints(values).astype(np.int64, copy=False))
+
+
 def _i32(values) -> np.ndarray:
-    if isinstance(values, torch.Tensor):
-        values = values.detach().cpu().numpy()
-    return np.ascontiguousarray(np.asarray(values, dtype=np.int32).reshape(-1))
+    a = _ints(values)
+    if a.size and (a.min() < np.iinfo(np.int32).min or a.max() > np.iinfo(np.int32).max):
+        raise ValueError("group ids must fit in 32 bits")
+    return np.ascontiguousarray(a.astype(np.int32, copy=False))
 
 
 def _p64(a: np.ndarray):

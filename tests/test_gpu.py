@@ -205,7 +205,7 @@ def test_threads_swap_concurrently_on_their_own_streams(gpu):
             dst = t * n + np.arange(n)
             for it in range(iters):
                 src = rng.permutation(n_gpu)[:n]
-                lay.swap(src, dst, np.zeros(n, np.int32), np.zeros(n), np.ones(n), False,
+                lay.swap(src, dst, np.zeros(n, np.int32), np.zeros(n, np.int64), np.ones(n, np.int64), False,
                          mode=MODES[it % 2], stream=st)
                 st.synchronize()
                 mine = host[t * n:(t + 1) * n]
@@ -749,14 +749,14 @@ def test_runs_on_current_stream_and_orders_by_events(gpu):
     with torch.cuda.stream(side):
         ops.swap_segments([seg], [page], [0], [1], n, [1], pool.tensor, page, 0,
                           np.arange(n), np.arange(n)[::-1].copy(), np.zeros(n, np.int32),
-                          np.zeros(n), np.ones(n), False)
+                          np.zeros(n, np.int64), np.ones(n, np.int64), False)
         done = torch.cuda.Event()
         done.record(side)
     fresh = torch.zeros_like(seg)
     torch.cuda.current_stream().wait_event(done)
     ops.swap_segments([fresh], [page], [0], [1], n, [1], pool.tensor, page, 0,
                       np.arange(n)[::-1].copy(), np.arange(n), np.zeros(n, np.int32),
-                      np.zeros(n), np.ones(n), True)
+                      np.zeros(n, np.int64), np.ones(n, np.int64), True)
     torch.cuda.synchronize()
     assert torch.equal(fresh, seg)
     pool.free()
@@ -1267,8 +1267,8 @@ def test_fence_orders_a_swap_after_another_streams_write(gpu):
         seg.fill_(0x5A)
         ops.fence_signal(words, 1, 7)
     ops.fence_wait(words, 1, 7, flags, 0, timeout_s=30, stream=b)
-    lay.swap(np.arange(n), np.arange(n)[::-1].copy(), np.zeros(n, np.int32), np.zeros(n),
-             np.ones(n), False, stream=b)
+    lay.swap(np.arange(n), np.arange(n)[::-1].copy(), np.zeros(n, np.int32), np.zeros(n, np.int64),
+             np.ones(n, np.int64), False, stream=b)
     b.synchronize()
     assert int(flags[0]) == 0
     assert bool((pool.tensor == 0x5A).all()), "the swap ran before the fence was signalled"

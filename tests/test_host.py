@@ -251,6 +251,22 @@ def test_prepared_layout_rejects_host_segments():
         ops.SegmentLayout([], [], [], [], 4, [1], pool, 64, 0)
 
 
+def test_id_arrays_refuse_floats_and_wide_group_ids():
+    """Ids, extents and layout sizes are converted without truncation:
+    float or boolean arrays and group ids beyond 32 bits raise ValueError
+    (an empty list is an empty id array)."""
+    from aegaeon_amd import ops
+
+    assert ops._i64([]).dtype == np.int64 and ops._i64([]).size == 0
+    assert ops._i64(torch.tensor([3, 4])).tolist() == [3, 4]
+    assert ops._i32(np.array([2], np.uint8)).dtype == np.int32
+    for bad in ([1.5], np.array([True]), torch.tensor([2.0])):
+        with pytest.raises(ValueError, match="integers"):
+            ops._i64(bad)
+    with pytest.raises(ValueError, match="32 bits"):
+        ops._i32([1 << 32])
+
+
 def test_fence_rejections_before_any_hip_call(aegkv_lib):
     from aegaeon_amd import _lib
 
