@@ -45,6 +45,7 @@ TUNE_COPY_LDS_BYTES = 11
 TUNE_SWAP_UNROLL = 12
 TUNE_STAGED_WORKGROUPS = 13
 TUNE_STAGED_OVERLAP = 14
+TUNE_SWAP_OUT_WORKGROUPS_UNCACHED = 15
 HOST_UNCACHED = 1
 
 #: every symbol include/aegkv.h declares

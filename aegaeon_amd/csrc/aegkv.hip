@@ -78,6 +78,11 @@ struct Tunables {
   // slower) and leave the other CUs to concurrent copies.
   int64_t swap_out_workgroups = 32;
   int64_t swap_in_workgroups = 64;
+  // Swap-out into an uncached pool: alone any of 32-64 workgroups runs at
+  // the link rate (57.1 GB/s), and beside a swap-in 56 leave the swap-in
+  // more of the link (model switch 108.5 -> 105 ms). Into a cached pool 32
+  // stay best alone (56.6 vs 55.8 GB/s at 64) and equal beside a swap-in.
+  int64_t swap_out_workgroups_uncached = 56;
   int64_t staging_bytes = int64_t(512) << 20;
   int64_t auto_d2h = AEGKV_MODE_DIRECT;
   int64_t auto_h2d = AEGKV_MODE_DIRECT;
@@ -524,6 +529,17 @@ int check_host_range(const void* ptr, int64_t bytes, const char* what) {
                 what, ptr);
   }
   return 0;
+}
+
+// True when p lies in a pool from aegkv_host_alloc_flags(AEGKV_HOST_UNCACHED).
+bool in_uncached_pool(const void* p) {
+  std::lock_guard<std::mutex> lk(g_host_mu);
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  auto it = g_uncached.upper_bound(a);
+  if (it == g_uncached.begin()) return false;
+  --it;
+  return a >= it->first && a < it->first + it->second &&
+         g_host_allocs.count(it->first) != 0;
 }
 
 // ----------------------------------------------------------- launching --
@@ -1116,11 +1132,12 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   if (!staged) {
     std::lock_guard<std::mutex> lk(ctx->mu);
     // link-bound: a few persistent workgroups
+    const int64_t wgs = is_swap_in                        ? t.swap_in_workgroups
+                        : in_uncached_pool(L.host_pool) ? t.swap_out_workgroups_uncached
+                                                        : t.swap_out_workgroups;
     return enqueue_swap_kernel(ctx, L, E, order, 0, order.size(), is_swap_in, false,
                                L.host_pool, L.host_page_bytes, L.host_rank_offset,
-                               dev_vec && host_vec,
-                               is_swap_in ? t.swap_in_workgroups : t.swap_out_workgroups,
-                               stream);
+                               dev_vec && host_vec, wgs, stream);
   }
 
   // STAGED: host-id order lets consecutive host pages merge into one DMA.
@@ -1286,6 +1303,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_STAGED_DMA_STREAMS: slot = &g_tune.staged_dma_streams; break;
     case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
     case AEGKV_TUNE_STAGED_OVERLAP: slot = &g_tune.staged_overlap; break;
+    case AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED: slot = &g_tune.swap_out_workgroups_uncached; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -1293,7 +1311,8 @@ int64_t aegkv_tune(int key, int64_t value) {
     if ((key == AEGKV_TUNE_AUTO_D2H || key == AEGKV_TUNE_AUTO_H2D) &&
         value != AEGKV_MODE_DIRECT && value != AEGKV_MODE_STAGED)
       return fail(AEGKV_EINVAL, "AUTO must resolve to DIRECT or STAGED");
-    if ((key == AEGKV_TUNE_SWAP_OUT_WORKGROUPS || key == AEGKV_TUNE_SWAP_IN_WORKGROUPS) &&
+    if ((key == AEGKV_TUNE_SWAP_OUT_WORKGROUPS || key == AEGKV_TUNE_SWAP_IN_WORKGROUPS ||
+         key == AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) &&
         (value < 1 || value > 65536))
       return fail(AEGKV_EINVAL, "swap workgroups must be in [1, 65536]");
     if (key == AEGKV_TUNE_STAGING_BYTES && value < (int64_t(1) << 20))
@@ -1396,6 +1415,8 @@ int aegkv_stream_create(hipStream_t* stream) {
 int aegkv_stream_destroy(hipStream_t stream) {
   g_err[0] = '\0';
   if (!stream) return fail(AEGKV_EINVAL, "stream must not be null");
+  // the stream's queued work finishes first, whatever the caller dropped
+  AEGKV_HIP(hipStreamSynchronize(stream));
   AEGKV_HIP(hipStreamDestroy(stream));
   return 0;
 }

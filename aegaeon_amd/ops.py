@@ -358,6 +358,27 @@ def migrate_blocks(
     _lib.check(rc)
 
 
+class _OwnedStream(torch.cuda.ExternalStream):
+    """A torch stream over a HIP stream from aegkv_stream_create that
+    destroys the HIP stream when the object goes (or on _aegkv_close()).
+    weakref.finalize is not used: its callback was seen not to run for
+    torch stream objects."""
+
+    def __init__(self, stream_ptr: int, device=None):
+        self._aegkv_ptr = stream_ptr
+
+    def _aegkv_close(self) -> None:
+        ptr, self._aegkv_ptr = getattr(self, "_aegkv_ptr", None), None
+        if ptr:
+            _lib.load().aegkv_stream_destroy(ctypes.c_void_p(ptr))
+
+    def __del__(self):
+        try:
+            self._aegkv_close()
+        except Exception:  # interpreter shutdown: the process is ending anyway
+            pass
+
+
 class DedicatedStream:
     """A HIP stream on a hardware queue of its own (aegkv_stream_create),
     usable wherever torch takes a stream through `.stream`.
@@ -368,8 +389,10 @@ class DedicatedStream:
     Unlike torch's pool streams, a dedicated stream is a blocking stream: it
     synchronizes with the legacy default (null) stream, so work on it waits
     for the default stream's earlier work and the other way round.
-    The HIP stream lives while this object or its `.stream` is referenced
-    and is destroyed by close() or when both are gone.
+    The HIP stream lives exactly as long as the `.stream` object (which this
+    object holds): it is destroyed by close() or as soon as the last
+    reference to `.stream` goes, after its queued work, so dropped streams
+    do not keep hardware queues until a garbage collection.
     """
 
     def __init__(self, device: torch.device | None = None):
@@ -378,14 +401,10 @@ class DedicatedStream:
         ptr = ctypes.c_void_p()
         _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create(ctypes.byref(ptr))))
         self.device = dev
-        self.stream = torch.cuda.ExternalStream(ptr.value, device=dev)
-        # the stream object keeps its owner alive, so `.stream` alone is
-        # enough to hold the HIP stream
-        self.stream._aegkv_owner = self
-        self._fin = weakref.finalize(self, lib.aegkv_stream_destroy, ptr.value)
+        self.stream = _OwnedStream(ptr.value, device=dev)
 
     def close(self) -> None:
-        self._fin()
+        self.stream._aegkv_close()
 
 
 def _free_pinned(ptr: int) -> None:

@@ -306,6 +306,18 @@ class KVSwapper:
                     "source fence that was never signalled; swaps after that wait may have "
                     "read data before its producer wrote it")
 
+    def close(self) -> None:
+        """Wait for this swapper's swaps and release its dedicated streams,
+        if it has any (their hardware queues are returned at once). The
+        swapper is not usable afterwards."""
+        for st in (self.swap_in_stream, self.swap_out_stream):
+            if st is not None:
+                st.synchronize()
+        for owner in self._streams:
+            owner.close()
+        self._streams = []
+        self.swap_in_stream = self.swap_out_stream = None
+
     def wait_for_all_move_in(self) -> None:
         self.swap_in_stream.synchronize()
         self._check_fences(1, self.swap_in_stream)

@@ -532,6 +532,8 @@ def bench_switch(args):
     wall = statistics.median(r[0] for r in runs)
     host_ms = statistics.median(r[1] for r in runs) * 1e3
     moved = statistics.median(r[2] + r[3] for r in runs)
+    for s in sw:
+        s.close()
     host.free()
     return {
         "metric": "model-switch wall time and link rate through planner + swapper + ledger",

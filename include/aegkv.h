@@ -88,6 +88,8 @@ extern "C" {
                                         staging chunks in flight, bit 0 for
                                         swap-out, bit 1 for swap-in
                                         (default 2)                        */
+#define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
+                                        uncached pool: workgroups (56)     */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);
@@ -231,6 +233,7 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
  * can lose their overlap; a stream created with a CU mask gets a queue to
  * itself (the mask here enables every CU). Default priority. It is a
  * blocking stream: it synchronizes with the legacy default (null) stream.
+ * aegkv_stream_destroy waits for the stream's queued work, then destroys it.
  */
 int aegkv_stream_create(hipStream_t* stream);
 int aegkv_stream_destroy(hipStream_t stream);

@@ -337,7 +337,8 @@ def restore_tuning():
     keys = (_lib.TUNE_COPY_UNROLL, _lib.TUNE_COPY_WGS_PER_CU, _lib.TUNE_SWAP_SHAPE_AUTO,
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
             _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
-            _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS, _lib.TUNE_STAGED_OVERLAP)
+            _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS, _lib.TUNE_STAGED_OVERLAP,
+            _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -373,6 +374,7 @@ def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, u
     _lib.tune(_lib.TUNE_SWAP_SHAPE_AUTO, shape_auto)
     _lib.tune(_lib.TUNE_SWAP_UNROLL, unroll)
     _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS, wpc)
+    _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, wpc)
     _lib.tune(_lib.TUNE_SWAP_IN_WORKGROUPS, wpc)
     rng = np.random.default_rng(31 + wpc)
     page = np.array([160 * 1024, 32 * 1024, 4096, 48 * 1024 + 16 * 4], np.int64)
@@ -1223,7 +1225,9 @@ def test_migrate_from_another_process_cache(gpu):
 
 def test_dedicated_stream_lives_with_its_torch_stream(gpu):
     """A DedicatedStream's `.stream` keeps the HIP stream alive after the
-    owner object is dropped; work on it completes and orders normally."""
+    owner object is dropped; work on it completes and orders normally; the
+    HIP stream is destroyed as soon as the last reference to `.stream` goes
+    (no garbage collection needed), and close() releases it explicitly."""
     import gc
 
     st = ops.DedicatedStream(gpu).stream
@@ -1235,9 +1239,17 @@ def test_dedicated_stream_lives_with_its_torch_stream(gpu):
         done.record(st)
     torch.cuda.current_stream().wait_event(done)
     assert int((y - 3 * x).abs().sum()) == 0
-    owner = st._aegkv_owner
+    import weakref
+
+    ref = weakref.ref(st)
+    assert st._aegkv_ptr
+    torch.cuda.synchronize()
     del st
-    owner.close()                                   # explicit release is also fine
+    assert ref() is None                            # destroyed with its last reference
+    owner = ops.DedicatedStream(gpu)
+    owner.close()                                   # explicit release, once
+    assert owner.stream._aegkv_ptr is None
+    owner.close()
 
 
 # ------------------------------------------------------------------ fences --

@@ -303,6 +303,9 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 4
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
     assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 2
+    assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 56
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_STAGED_OVERLAP, 4)
     with pytest.raises(ValueError):
