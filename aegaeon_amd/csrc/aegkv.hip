@@ -73,16 +73,21 @@ int hip_fail(hipError_t e, const char* what) {
 // --------------------------------------------------------------- tunables --
 
 struct Tunables {
-  // Swap kernels: persistent workgroups in total, per direction. The swaps
-  // are link-bound; a few dozen workgroups saturate PCIe (more measured
-  // slower) and leave the other CUs to concurrent copies.
-  int64_t swap_out_workgroups = 32;
-  int64_t swap_in_workgroups = 64;
-  // Swap-out into an uncached pool: alone any of 32-64 workgroups runs at
-  // the link rate (57.1 GB/s), and beside a swap-in 56 leave the swap-in
-  // more of the link (model switch 108.5 -> 105 ms). Into a cached pool 32
-  // stay best alone (56.6 vs 55.8 GB/s at 64) and equal beside a swap-in.
-  int64_t swap_out_workgroups_uncached = 56;
+  // Swap kernels: persistent workgroups in total, per direction, each lane
+  // with swap_unroll 16 B loads in flight. The swaps are link-bound: about
+  // 1 MiB in flight per direction saturates PCIe, and the few workgroups
+  // leave the other CUs to concurrent copies. Two loads per lane with twice
+  // the workgroups keep the same bytes in flight and share the link better
+  // when both directions run at once (model switch 105 -> 103 ms), at the
+  // same rate for one direction alone (57.1 / 57.5 GB/s).
+  int64_t swap_out_workgroups = 64;
+  int64_t swap_in_workgroups = 128;
+  // Swap-out into an uncached pool: alone 64-224 workgroups all reach the
+  // link rate, and beside a swap-in 112 leave the swap-in more of the link
+  // (with 4 loads per lane: 32 -> 56 workgroups, 108.5 -> 105 ms). Into a
+  // cached pool 64 stay best alone (56.6 GB/s; 55.8 at 112) and equal
+  // beside a swap-in.
+  int64_t swap_out_workgroups_uncached = 112;
   int64_t staging_bytes = int64_t(512) << 20;
   int64_t auto_d2h = AEGKV_MODE_DIRECT;
   int64_t auto_h2d = AEGKV_MODE_DIRECT;
@@ -90,7 +95,7 @@ struct Tunables {
   int64_t copy_wgs_per_cu = 0;   // copy_blocks: 0 = one workgroup per work item
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
-  int64_t swap_unroll = 4;       // swap kernels: 16 B loads per lane (256-lane shape)
+  int64_t swap_unroll = 2;       // swap kernels: 16 B loads per lane (256-lane shape)
   int64_t staged_workgroups = 0; // STAGED gather/scatter grid: 0 = one workgroup per item
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
   // STAGED over library streams: two staging chunks in flight (bit 0

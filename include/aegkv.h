@@ -81,7 +81,8 @@ extern "C" {
                                         per workgroup (0 - 160 KiB; caps
                                         workgroups per CU; default 96 KiB) */
 #define AEGKV_TUNE_SWAP_UNROLL 12    /* swap kernels: 16 B loads per lane of
-                                        the 256-lane shape (1, 2 or 4)      */
+                                        the 256-lane shape (1, 2 or 4;
+                                        default 2)                         */
 #define AEGKV_TUNE_STAGED_WORKGROUPS 13 /* STAGED gather/scatter grid (0 = one
                                            workgroup per item)             */
 #define AEGKV_TUNE_STAGED_OVERLAP 14 /* STAGED over library streams: two
@@ -89,7 +90,7 @@ extern "C" {
                                         swap-out, bit 1 for swap-in
                                         (default 2)                        */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
-                                        uncached pool: workgroups (56)     */
+                                        uncached pool: workgroups (112)    */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -300,10 +300,10 @@ def test_tuning_knobs(aegkv_lib):
     with pytest.raises(ValueError):
         _lib.tune(99, 1)
     assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
-    assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 4
+    assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 2
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
     assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 2
-    assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 56
+    assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 112
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):
