@@ -64,6 +64,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_fence_signal",
     "aegkv_fence_wait",
     "aegkv_stream_create",
+    "aegkv_stream_create_masked",
     "aegkv_stream_destroy",
 )
 
@@ -99,6 +100,7 @@ _SIGNATURES = {
     "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
     "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),
     "aegkv_stream_create": (_INT, [_PP]),
+    "aegkv_stream_create_masked": (_INT, [_PP, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]),
     "aegkv_stream_destroy": (_INT, [_P]),
 }
 

@@ -1417,6 +1417,34 @@ int aegkv_stream_create(hipStream_t* stream) {
   return 0;
 }
 
+int aegkv_stream_create_masked(hipStream_t* stream, const uint32_t* cu_mask,
+                               int32_t mask_words) {
+  g_err[0] = '\0';
+  if (!stream) return fail(AEGKV_EINVAL, "stream pointer must not be null");
+  if (!cu_mask || mask_words <= 0) return fail(AEGKV_EINVAL, "CU mask must not be empty");
+  int dev = -1, cus = 0;
+  AEGKV_HIP(hipGetDevice(&dev));
+  AEGKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  int64_t set = 0;
+  for (int32_t w = 0; w < mask_words; ++w)
+    for (int b = 0; b < 32; ++b)
+      if ((cu_mask[w] >> b) & 1u) {
+        if (int64_t(w) * 32 + b >= cus)
+          return fail(AEGKV_ERANGE, "CU mask names CU %d; the device has %d", w * 32 + b, cus);
+        ++set;
+      }
+  if (set == 0) return fail(AEGKV_EINVAL, "CU mask enables no CU");
+  hipError_t e = hipExtStreamCreateWithCUMask(stream, static_cast<uint32_t>(mask_words), cu_mask);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(static_cast<int>(e),
+                "hipExtStreamCreateWithCUMask refused the mask (%s); the runtime takes runs "
+                "of 8 or more consecutive CUs starting at a multiple of 8",
+                hipGetErrorString(e));
+  }
+  return 0;
+}
+
 int aegkv_stream_destroy(hipStream_t stream) {
   g_err[0] = '\0';
   if (!stream) return fail(AEGKV_EINVAL, "stream must not be null");

@@ -379,6 +379,28 @@ class _OwnedStream(torch.cuda.ExternalStream):
             pass
 
 
+CUS_PER_XCD = 32  # MI355X (gfx950): 8 XCDs of 32 CUs
+
+
+def xcd_cu_mask(cus_per_xcd: int, first: int = 0,
+                device: torch.device | None = None) -> list[int]:
+    """CU mask words (for DedicatedStream(cu_mask=...)) that enable CUs
+    [first, first + cus_per_xcd) of every 32-CU XCD, so the work spreads
+    over all XCDs. The runtime accepts runs of 8 or more CUs starting at a
+    multiple of 8, e.g. xcd_cu_mask(8) for the swap streams and
+    xcd_cu_mask(24, first=8) for the rest."""
+    if cus_per_xcd <= 0 or first < 0 or first + cus_per_xcd > CUS_PER_XCD:
+        raise ValueError(f"CUs [{first}, {first + cus_per_xcd}) do not fit a "
+                         f"{CUS_PER_XCD}-CU XCD")
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    n = torch.cuda.get_device_properties(dev).multi_processor_count
+    words = [0] * ((n + 31) // 32)
+    for i in range(n):
+        if first <= i % CUS_PER_XCD < first + cus_per_xcd:
+            words[i // 32] |= 1 << (i % 32)
+    return words
+
+
 class DedicatedStream:
     """A HIP stream on a hardware queue of its own (aegkv_stream_create),
     usable wherever torch takes a stream through `.stream`.
@@ -386,6 +408,7 @@ class DedicatedStream:
     Plain streams (torch.cuda.Stream included) share the process's 4
     hardware queues, and two streams on one queue run their work one after
     the other; a swap-out and a swap-in on dedicated streams always overlap.
+    With cu_mask (see xcd_cu_mask) its kernels run only on those CUs.
     Unlike torch's pool streams, a dedicated stream is a blocking stream: it
     synchronizes with the legacy default (null) stream, so work on it waits
     for the default stream's earlier work and the other way round.
@@ -395,12 +418,19 @@ class DedicatedStream:
     do not keep hardware queues until a garbage collection.
     """
 
-    def __init__(self, device: torch.device | None = None):
+    def __init__(self, device: torch.device | None = None, cu_mask: Sequence[int] | None = None):
         dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
         lib = _lib.load()
         ptr = ctypes.c_void_p()
-        _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create(ctypes.byref(ptr))))
+        if cu_mask is None:
+            _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create(ctypes.byref(ptr))))
+        else:
+            words = np.ascontiguousarray(np.asarray(cu_mask, dtype=np.uint32).reshape(-1))
+            arg = words.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32))
+            _lib.check(_call_on(dev, lambda: lib.aegkv_stream_create_masked(
+                ctypes.byref(ptr), arg, int(words.size))))
         self.device = dev
+        self.cu_mask = None if cu_mask is None else list(cu_mask)
         self.stream = _OwnedStream(ptr.value, device=dev)
 
     def close(self) -> None:

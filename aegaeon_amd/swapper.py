@@ -58,7 +58,8 @@ class KVSwapper:
                  host_element_size: int = 2, interprocess_events: bool = False,
                  fence_words: Optional[torch.Tensor] = None,
                  fence_slots: Optional[Tuple[int, int]] = None,
-                 fence_timeout_s: float = 30.0, dedicated_streams: bool = False):
+                 fence_timeout_s: float = 30.0, dedicated_streams: bool = False,
+                 swap_cu_mask: Optional[Sequence[int]] = None):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -122,8 +123,13 @@ class KVSwapper:
         # streams also synchronize with the legacy default (null) stream, so
         # they suit processes whose other GPU work runs on non-default
         # streams.
+        # swap_cu_mask (ops.xcd_cu_mask) confines the swap kernels to those
+        # CUs, leaving the others to HBM-bound work on other streams.
+        if swap_cu_mask is not None and not dedicated_streams:
+            raise ValueError("swap_cu_mask needs dedicated_streams=True")
         if dedicated_streams:
-            self._streams = [ops.DedicatedStream(device), ops.DedicatedStream(device)]
+            self._streams = [ops.DedicatedStream(device, swap_cu_mask),
+                             ops.DedicatedStream(device, swap_cu_mask)]
             self.swap_in_stream = self._streams[0].stream
             self.swap_out_stream = self._streams[1].stream
         else:

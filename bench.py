@@ -57,6 +57,8 @@ def parse():
     p.add_argument("--no-switch", action="store_true",
                    help="skip the model-switch line (both link directions at once)")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--no-cu-partition", action="store_true",
+                   help="overlap config: run the three streams on every CU")
     p.add_argument("--no-side-by-side", action="store_true",
                    help="skip the DIRECT vs STAGED side-by-side measurement")
     p.add_argument("--no-reference-loop", action="store_true",
@@ -320,7 +322,13 @@ def bench_overlap(args):
 
     dev = torch.device("cuda:0")
     _lib.load()
-    owners = [ops.DedicatedStream(dev) for _ in range(3)]
+    # CU partition: the link-bound swap kernels on CUs 0-7 of every XCD, the
+    # HBM-bound copy on CUs 8-31, so the copy does not share CUs with waves
+    # that wait on PCIe (without it the copy ran 150-200 ms instead of 11)
+    partition = not getattr(args, "no_cu_partition", False)
+    masks = ([ops.xcd_cu_mask(8, device=dev)] * 2 + [ops.xcd_cu_mask(24, 8, device=dev)]
+             if partition else [None] * 3)
+    owners = [ops.DedicatedStream(dev, m) for m in masks]
     bidir = measure_link_bidir(torch, ops, dev)
     L, NB, H, D = 24, 32768, 16, 128
     NOUT, NIN, NP = 16384, 12288, 2048
@@ -405,7 +413,9 @@ def bench_overlap(args):
         "config": {"workload": f"Qwen1.5-MoE KV 48 x [32768,16,16,128] bf16; swap-out {NOUT}, "
                                f"swap-in {NIN}, copy_blocks {NP} pairs, one stream each",
                    "bytes": {"d2h": b_out, "h2d": b_in, "copy_rw": b_cp},
-                   "swap_block_scale": scale, "blocks": {"d2h": NOUT, "h2d": NIN, "pairs": NP}},
+                   "swap_block_scale": scale, "blocks": {"d2h": NOUT, "h2d": NIN, "pairs": NP},
+                   "cu_partition": ("swap streams on CUs 0-7 of each XCD, copy stream on CUs 8-31"
+                                    if partition else None)},
         "d2h_GBps": round(b_out / t_out / 1e9, 3),
         "h2d_GBps": round(b_in / t_in / 1e9, 3),
         "copy_blocks_GBps": round(b_cp / t_cp / 1e9, 1),

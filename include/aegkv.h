@@ -240,6 +240,18 @@ int aegkv_stream_create(hipStream_t* stream);
 int aegkv_stream_destroy(hipStream_t stream);
 
 /*
+ * The same, on a subset of the CUs: bit i of cu_mask (mask_words 32-bit
+ * words) enables CU i. Kernels launched on the stream run only there, so
+ * link-bound swap waves can be kept off the CUs that HBM-bound work (block
+ * copies, the model's kernels) uses on other streams. No counterpart in the
+ * reference. The runtime accepts runs of 8 or more consecutive CUs that
+ * start at a multiple of 8 (CUs are numbered 32 per XCD); it refuses finer
+ * masks with a positive hipError_t status.
+ */
+int aegkv_stream_create_masked(hipStream_t* stream, const uint32_t* cu_mask,
+                               int32_t mask_words);
+
+/*
  * Pinned host pool. Replaces the pinning half of the reference's host KV
  * pool set-up: Controller._init_cpu_cache (aegaeon/llm.py:1020-1040) and
  * the worker's cudaHostRegister of that mapping (aegaeon/worker.py:251-273).

@@ -766,9 +766,12 @@ def test_runs_on_current_stream_and_orders_by_events(gpu):
 
 # ------------------------------------------------------------ swapper --
 
-def test_swapper_block_table_round_trip(gpu, oracle):
+@pytest.mark.parametrize("streams", ["pool", "dedicated", "partitioned"])
+def test_swapper_block_table_round_trip(gpu, oracle, streams):
     """BlockTable.transfer_entries -> KVSwapper.swap_blocks out and back in,
-    partial extents included, checked against the oracle."""
+    partial extents included, checked against the oracle; on torch pool
+    streams, dedicated streams, and dedicated streams on CUs 0-7 of every
+    XCD."""
     from aegaeon_amd.cache_groups import BlockTable, CacheGroupConfig, CacheGroupRuntimeConfig
     from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
     from aegaeon_amd.swapper import KVSwapper
@@ -785,7 +788,9 @@ def test_swapper_block_table_round_trip(gpu, oracle):
              CacheGroupRuntimeConfig("attention", 64, 16, 40)]
     pool = ops.PinnedHostPool(n_host * cache.page_size_bytes)
     pool.tensor.zero_()
-    sw = KVSwapper(cache, [{"full.0", "full.1"}, {"win.0", "win.1"}], descr, pool.tensor)
+    sw = KVSwapper(cache, [{"full.0", "full.1"}, {"win.0", "win.1"}], descr, pool.tensor,
+                   dedicated_streams=streams != "pool",
+                   swap_cu_mask=ops.xcd_cu_mask(8) if streams == "partitioned" else None)
     table = BlockTable(0, (cache.page_size_bytes // 2,), groups,
                        [[3, 4, 5, 6], [7, 8, 9, 10]])
     tokens = 230
@@ -816,6 +821,8 @@ def test_swapper_block_table_round_trip(gpu, oracle):
     for t, w in zip(cache.backing, before):
         assert np.array_equal(t.cpu().numpy().view(np.uint8), w)
     assert ev2.query()
+    sw.close()
+    assert sw.swap_in_stream is None
     pool.free()
 
 
@@ -1250,6 +1257,37 @@ def test_dedicated_stream_lives_with_its_torch_stream(gpu):
     owner.close()                                   # explicit release, once
     assert owner.stream._aegkv_ptr is None
     owner.close()
+
+
+def test_swaps_and_copy_on_cu_partitioned_streams(gpu):
+    """Swap streams on CUs 0-7 of every XCD and a copy_blocks stream on CUs
+    8-31, running at once: every block lands where the closed form says."""
+    swap_mask = ops.xcd_cu_mask(8)
+    copy_mask = ops.xcd_cu_mask(24, first=8)
+    assert all(a & b == 0 for a, b in zip(swap_mask, copy_mask))
+    n_gpu, page, n, S = 256, 32768, 96, 6
+    segs = [torch.randint(0, 256, (n_gpu, page), dtype=torch.uint8, device=gpu) for _ in range(S)]
+    before = [x.clone() for x in segs]
+    pool = ops.PinnedHostPool(n * S * page)
+    lay = ops.SegmentLayout(segs, [page] * S, [i * page for i in range(S)], [1] * S, n_gpu, [1],
+                            pool.tensor, S * page, 0)
+    perm = np.random.default_rng(61).permutation(n_gpu)
+    out_ids, csrc, cdst = perm[:n], perm[n:n + 64], perm[n + 64:n + 128]
+    a, b = ops.DedicatedStream(gpu, swap_mask), ops.DedicatedStream(gpu, copy_mask)
+    z, one = np.zeros(n, np.int32), np.ones(n, np.int64)
+    torch.cuda.synchronize()
+    lay.swap(out_ids, np.arange(n), z, z, one, False, stream=a.stream)
+    ops.copy_blocks(segs, csrc, cdst, stream=b.stream)
+    torch.cuda.synchronize()
+    host = pool.tensor.view(n, S, page)
+    for s in range(S):
+        assert torch.equal(host[:, s].to(gpu), before[s][torch.from_numpy(out_ids).to(gpu)]), s
+        assert torch.equal(segs[s][torch.from_numpy(cdst).to(gpu)],
+                           before[s][torch.from_numpy(csrc).to(gpu)]), s
+    a.close()
+    b.close()
+    del lay
+    pool.free()
 
 
 # ------------------------------------------------------------------ fences --

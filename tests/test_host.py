@@ -267,6 +267,24 @@ def test_id_arrays_refuse_floats_and_wide_group_ids():
         ops._i32([1 << 32])
 
 
+def test_masked_stream_rejections_before_any_hip_call(aegkv_lib):
+    """aegkv_stream_create_masked refuses a missing stream pointer or an
+    empty mask before touching the device; xcd_cu_mask refuses CU ranges
+    that do not fit a 32-CU XCD."""
+    from aegaeon_amd import _lib, ops
+
+    lib = aegkv_lib
+    st = ctypes.c_void_p()
+    words = (ctypes.c_uint32 * 1)(0xFF)
+    assert lib.aegkv_stream_create_masked(None, words, 1) == _lib.EINVAL
+    assert lib.aegkv_stream_create_masked(ctypes.byref(st), None, 1) == _lib.EINVAL
+    assert lib.aegkv_stream_create_masked(ctypes.byref(st), words, 0) == _lib.EINVAL
+    assert b"empty" in lib.aegkv_last_error()
+    for cus, first in ((0, 0), (8, 28), (33, 0), (8, -1)):
+        with pytest.raises(ValueError, match="XCD"):
+            ops.xcd_cu_mask(cus, first)
+
+
 def test_fence_rejections_before_any_hip_call(aegkv_lib):
     from aegaeon_amd import _lib
 
