@@ -65,14 +65,15 @@ def parse():
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
     p.add_argument("--config", default="headline",
-                   choices=["headline", "varlen", "overlap", "refplan", "switch"],
+                   choices=["headline", "varlen", "overlap", "refplan", "switch", "serving"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
                         "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
                         "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams; "
                         "refplan: the reference benchmark's extent plans, libaegkv beside "
                         "the reference's per-extent copy_ loop on the same GPU; switch: "
                         "two models' KV swapped out and in at once through the planner, "
-                        "swapper and move ledger")
+                        "swapper and move ledger; serving: a bf16 GEMM loop beside both "
+                        "swaps, for the default and a smaller swap grid")
     return p.parse_args()
 
 
@@ -565,6 +566,104 @@ def bench_switch(args):
     }
 
 
+def bench_serving(args):
+    """Swaps beside model compute: a bf16 8192 x 8192 x 8192 GEMM loop
+    (torch.mm, 40 products) on its own stream while the Qwen3-4B swap-out
+    and swap-in of 1024 blocks run on two more streams, all started
+    together on streams with hardware queues of their own. Reported: the
+    GEMM's TFLOP/s alone and beside the swaps, and the swap rates, for the
+    default swap grid and for a smaller one (24 workgroups per direction,
+    4 loads per lane)."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    L, NB, H, D, HOST, N = 36, 8192, 8, 128, 4096, 1024
+    segs = kv_segments(torch, L, NB, H, D, torch.bfloat16, dev, 1)
+    S = len(segs)
+    tile = 16 * H * D * 2
+    page = S * tile
+    g = torch.Generator().manual_seed(1)
+    out_ids = (torch.randperm(NB - 1, generator=g)[:N] + 1).numpy()
+    host_ids = torch.randperm(HOST, generator=g)[:N].numpy()
+    rest = np.setdiff1d(np.arange(1, NB), out_ids)
+    in_ids = rest[torch.randperm(rest.size, generator=g)[:N].numpy()]
+    host_in = np.setdiff1d(np.arange(HOST), host_ids)[:N]
+    z, one = np.zeros(N, np.int32), np.ones(N, np.int64)
+    pool = ops.PinnedHostPool(HOST * page, uncached=True)
+    lay = ops.SegmentLayout(segs, [tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1],
+                            pool.tensor, page, 0)
+    lay.swap(in_ids, host_in, z, z, one, False)      # the incoming blocks, parked on the host
+    M, iters = 8192, 40
+    a = torch.randn(M, M, device=dev, dtype=torch.bfloat16)
+    b = torch.randn(M, M, device=dev, dtype=torch.bfloat16)
+    c = torch.empty(M, M, device=dev, dtype=torch.bfloat16)
+    flops = iters * 2 * M ** 3
+    streams = [ops.DedicatedStream(dev) for _ in range(3)]
+    gemm_st, out_st, in_st = (x.stream for x in streams)
+    with torch.cuda.stream(gemm_st):
+        for _ in range(3):
+            torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+
+    def once(with_swaps):
+        begin = torch.cuda.Event(enable_timing=True)
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        torch.cuda.synchronize()
+        begin.record()
+        for st in (gemm_st, out_st, in_st):
+            st.wait_event(begin)
+        with torch.cuda.stream(gemm_st):
+            for _ in range(iters):
+                torch.mm(a, b, out=c)
+            ends[0].record()
+        if with_swaps:
+            lay.swap(out_ids, host_ids, z, z, one, False, stream=out_st)
+            ends[1].record(out_st)
+            lay.swap(host_in, in_ids, z, z, one, True, stream=in_st)
+            ends[2].record(in_st)
+        torch.cuda.synchronize()
+        t = [begin.elapsed_time(e) / 1e3 for e in ends[:3 if with_swaps else 1]]
+        return [flops / t[0] / 1e12] + [N * page / x / 1e9 for x in t[1:]]
+
+    def median3(with_swaps):
+        runs = [once(with_swaps) for _ in range(3)]
+        return [round(statistics.median(r[i] for r in runs), 2) for i in range(len(runs[0]))]
+
+    keys = (_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_SWAP_IN_WORKGROUPS,
+            _lib.TUNE_SWAP_UNROLL)
+    saved = [_lib.tune(k) for k in keys]
+    out = {"gemm_alone_TFLOPs": median3(False)[0]}
+    for name, grid in (("default_grid", saved), ("grid_24x4", (24, 24, 4))):
+        for k, v in zip(keys, grid):
+            _lib.tune(k, int(v))
+        gemm, d2h, h2d = median3(True)
+        out[name] = {"workgroups_out_in_unroll": [int(v) for v in grid], "gemm_TFLOPs": gemm,
+                     "swap_out_GBps": d2h, "swap_in_GBps": h2d}
+    for k, v in zip(keys, saved):
+        _lib.tune(k, v)
+    di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
+    pages = pool.tensor.view(HOST, S, tile)
+    ok = all(torch.equal(pages[int(host_ids[k]), s].to(dev),
+                         segs[s][int(out_ids[k])].view(torch.uint8).reshape(-1))
+             for k in (0, N // 2, N - 1) for s in (0, S - 1))
+    if not ok:
+        raise AssertionError("serving config: swapped pages are not bit-exact")
+    for x in streams:
+        x.close()
+    del lay
+    pool.free()
+    return {"metric": "model GEMM TFLOP/s and swap GB/s when both run at once",
+            "config": {"workload": "bf16 8192^3 torch.mm x 40 beside the Qwen3-4B swap-out and "
+                                   "swap-in of 1024 blocks (72 x [8192,16,8,128] bf16, uncached "
+                                   "4096-block pool)", "runs": 3, "statistic": "median"},
+            **out, "bit_exact": True}
+
+
 def reference_submit_copies(cpu_pages, gpu_segments, extents, is_swap_in):
     """The reference benchmark's copy loop (benchmark_composite_swap.py:67-87):
     one narrow().copy_(non_blocking=True) per (segment, page) extent."""
@@ -752,8 +851,8 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.config != "headline":
-        fn = {"varlen": bench_varlen, "overlap": bench_overlap,
-              "refplan": bench_refplan, "switch": bench_switch}[args.config]
+        fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
+              "switch": bench_switch, "serving": bench_serving}[args.config]
         print(json.dumps(fn(args)), flush=True)
         return
     import numpy as np
