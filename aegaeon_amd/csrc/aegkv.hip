@@ -99,13 +99,15 @@ struct Tunables {
   int64_t staged_workgroups = 0; // STAGED gather/scatter grid: 0 = one workgroup per item
   int64_t staged_dma_streams = 2; // STAGED copies: library streams (<= 1: caller stream)
   // STAGED over library streams: two staging chunks in flight (bit 0
-  // swap-out, bit 1 swap-in). Swap-in gains either way (54.0 -> 55.3 GB/s
-  // scattered, 55.1 -> 56.4 contiguous). Swap-out gains (50.3 -> 54.3) only
-  // while the runtime runs its device-to-host copies as shader blits; when
-  // the host enqueues ahead of a busy GPU the runtime moved them to SDMA
-  // engines, where the overlapped swap-out fell to 24 GB/s against 33-40
-  // one chunk at a time, so swap-out stays serial by default.
-  int64_t staged_overlap = 2;
+  // swap-out, bit 1 swap-in), so the gather or scatter of one chunk runs
+  // while another chunk's copies use the link. Qwen3-4B, 1024 blocks (GB/s
+  // out / in): one call at a time 43.4 / 50.9 -> 54.3 / 55.4; swap-out and
+  // swap-in at once 174 -> 121 ms for a model switch; beside a GEMM the
+  // swaps end at 52 / 56 ms instead of 74 / 105. Where the host enqueues
+  // far ahead with block copies between the swaps, the runtime moved the
+  // swap-out's copies to SDMA and it fell to 29 GB/s (35 one chunk at a
+  // time); set bit 0 off for that pattern.
+  int64_t staged_overlap = 3;
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
   // 32-160 KiB tiles; 16 KiB items lose 14 % at one per CU, so they keep 0).
@@ -362,10 +364,11 @@ struct DeviceCtx {
   std::mutex mu;
   Ring ring;
   // STAGED mode: library-owned streams the per-run copies fan out over,
-  // forked from and joined back into the caller's stream with events. Both
-  // directions share the set: separate sets per direction add streams that
-  // share the process's 4 hardware queues with the callers' streams, and
-  // measured slower (one direction alone 50.0 -> 45.4-47.6 GB/s).
+  // forked from and joined back into the caller's stream with events, one
+  // set per direction (dma[0] swap-out, dma[1] swap-in) so a swap-out and
+  // a swap-in at once do not queue their copies behind each other (with
+  // one shared set, a swap-in beside a swap-out finished at 88-120 ms
+  // instead of 56 ms).
   // A staged call holds the set's mutex from its first fork to its last
   // join, so its events are not re-recorded by another call in between.
   struct DmaSet {
@@ -375,7 +378,7 @@ struct DeviceCtx {
     hipEvent_t fork_ev = nullptr;
     hipEvent_t join_ev[2][kMaxDmaStreams] = {};  // copies done, per staging buffer
     hipEvent_t kernel_ev[2] = {};                // gather / scatter done, per staging buffer
-  } dma;
+  } dma[2];
 };
 
 std::mutex g_ctx_mu;
@@ -960,6 +963,7 @@ int staged_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
 // holds) and joined back, which overlaps the runtime's per-copy gaps.
 int chunk_copies(DeviceCtx* ctx, int k, const std::vector<Run>& runs, bool to_device,
                  char* staging, char* host, hipStream_t stream) {
+  const int dir = to_device ? 1 : 0;
   if (k <= 1) {
     for (const Run& r : runs) {
       hipError_t e = copy_run(r, to_device, staging, host, stream);
@@ -967,7 +971,7 @@ int chunk_copies(DeviceCtx* ctx, int k, const std::vector<Run>& runs, bool to_de
     }
     return 0;
   }
-  DeviceCtx::DmaSet& d = ctx->dma;
+  DeviceCtx::DmaSet& d = ctx->dma[dir];
   std::lock_guard<std::mutex> lk(d.mu);
   int rc = ensure_dma(d, k);
   if (rc) return rc;
@@ -1029,7 +1033,7 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
                       const std::vector<int64_t>& order, bool is_swap_in, int64_t composite,
                       size_t step, bool vec_stage, const Tunables& t, int k,
                       hipStream_t stream) {
-  DeviceCtx::DmaSet& d = ctx->dma;
+  DeviceCtx::DmaSet& d = ctx->dma[is_swap_in ? 1 : 0];
   std::lock_guard<std::mutex> lk(d.mu);
   int rc = ensure_dma(d, k);
   if (rc) return rc;

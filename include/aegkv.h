@@ -88,7 +88,7 @@ extern "C" {
 #define AEGKV_TUNE_STAGED_OVERLAP 14 /* STAGED over library streams: two
                                         staging chunks in flight, bit 0 for
                                         swap-out, bit 1 for swap-in
-                                        (default 2)                        */
+                                        (default 3)                        */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
                                         uncached pool: workgroups (112)    */
 

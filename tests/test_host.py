@@ -320,7 +320,7 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_COPY_LDS_BYTES) == 96 * 1024
     assert _lib.tune(_lib.TUNE_SWAP_UNROLL) == 2
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
-    assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 2
+    assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 3
     assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 112
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
