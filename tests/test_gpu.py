@@ -574,6 +574,46 @@ def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     raw.free()
 
 
+def test_staged_swap_out_and_in_at_once(gpu, restore_tuning):
+    """A STAGED swap-out and a STAGED swap-in enqueued together on two
+    streams, each double-buffered over its own DMA streams with 8 MiB
+    chunks (67 chunks each way): the host pages and device tiles land as
+    the closed form says and nothing else changes."""
+    _lib.tune(_lib.TUNE_STAGING_BYTES, 8 << 20)
+    _lib.tune(_lib.TUNE_STAGED_OVERLAP, 3)
+    _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, 2)
+    segs = _kv_segments(36, 512, 8, 128, torch.bfloat16, gpu, 21)
+    tile = 16 * 8 * 128 * 2
+    S, n = len(segs), 200
+    pool = ops.PinnedHostPool(512 * S * tile)
+    host = pool.tensor.view(512, S, tile)
+    g = torch.Generator().manual_seed(22)
+    host.copy_(torch.randint(0, 256, host.shape, dtype=torch.uint8, generator=g))
+    perm = torch.randperm(512, generator=g).numpy()
+    out_ids, in_ids = perm[:n], perm[n:2 * n]
+    out_host, in_host = np.arange(n), np.arange(256, 256 + n)
+    want_in = host[torch.from_numpy(in_host)].to(gpu)            # what the swap-in brings
+    before = [x.clone() for x in segs]
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, 512, [1], pool.tensor, S * tile, 0)
+    lay = ops.SegmentLayout(segs, *common)
+    a, b = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    z, one = np.zeros(n, np.int32), np.ones(n, np.int64)
+    torch.cuda.synchronize()
+    lay.swap(out_ids, out_host, z, z, one, False, mode="staged", stream=a)
+    lay.swap(in_host, in_ids, z, z, one, True, mode="staged", stream=b)
+    torch.cuda.synchronize()
+    do, di = torch.from_numpy(out_ids).to(gpu), torch.from_numpy(in_ids).to(gpu)
+    got_out = host[torch.from_numpy(out_host)].to(gpu)
+    keep = torch.ones(512, dtype=torch.bool, device=gpu)
+    keep[di] = False
+    for s in range(S):
+        assert torch.equal(got_out[:, s], before[s][do].view(torch.uint8).reshape(n, -1)), s
+        assert torch.equal(segs[s][di].view(torch.uint8).reshape(n, -1), want_in[:, s]), s
+        assert torch.equal(segs[s][keep], before[s][keep]), s
+    del lay
+    pool.free()
+
+
 # ------------------------------------------------------- uncached host pool --
 
 @pytest.mark.parametrize("mode", MODES)
