@@ -17,7 +17,8 @@ directions' bytes over their summed time); the copy_blocks kernel carries
 the HBM roofline, the swaps the measured-host-link roofline. The line also
 reports the two host-transfer designs (DIRECT, STAGED) side by side on the
 same blocks, one call at a time, the reference's per-extent copy loop on the
-same GPU, and a model switch (both link directions at once).
+same GPU, a model switch (both link directions at once) and the swaps
+beside a GEMM loop (serving).
 
 The CPU baseline times the reference's torch path (one narrow().copy_() per
 (segment, block) extent, aegaeon/worker.py:2272-2328) on host tensors of the
@@ -57,6 +58,8 @@ def parse():
     p.add_argument("--no-switch", action="store_true",
                    help="skip the model-switch line (both link directions at once)")
     p.add_argument("--cpu-runs", type=int, default=5)
+    p.add_argument("--no-serving", action="store_true",
+                   help="skip the serving line (swaps beside a GEMM loop)")
     p.add_argument("--no-cu-partition", action="store_true",
                    help="overlap config: run the three streams on every CU")
     p.add_argument("--no-side-by-side", action="store_true",
@@ -1084,6 +1087,16 @@ def main():
             "link_aggregate_GBps", "link_bidirectional_ceiling_GBps",
             "frac_bidirectional_ceiling", "bit_exact")}
         line["model_switch"]["workload"] = sw["config"]["workload"]
+        torch.cuda.empty_cache()
+    # Swaps beside model compute (see --config serving): DIRECT or STAGED
+    # against a concurrent GEMM. Reported beside the metric.
+    line["serving"] = None
+    if not args.no_serving:
+        log("serving: swaps beside a bf16 GEMM loop")
+        sv = bench_serving(args)
+        line["serving"] = {k: sv[k] for k in ("gemm_alone_TFLOPs", "default_grid", "grid_24x4",
+                                              "staged", "bit_exact")}
+        line["serving"]["workload"] = sv["config"]["workload"]
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (reference torch path on host tensors)")
