@@ -45,14 +45,18 @@ extern "C" {
 #define AEGKV_EEXTENT (-4)       /* kernel-block extent outside the page     */
 #define AEGKV_EOVERLAP (-5)      /* copy: a source is also a target, or the
                                     migration's two caches overlap          */
-#define AEGKV_ENOMEM (-6)        /* descriptor larger than the upload ring   */
+#define AEGKV_ENOMEM (-6)        /* output arrays too small for the rows     */
 
 /* host-transfer designs for swap-out / swap-in */
-#define AEGKV_MODE_AUTO 0   /* library choice (per direction, measured)        */
+#define AEGKV_MODE_AUTO 0   /* library choice per direction: DIRECT unless
+                               AEGKV_AUTO_D2H / AEGKV_AUTO_H2D say otherwise */
 #define AEGKV_MODE_DIRECT 1 /* gather/scatter kernel reads/writes the pinned
                                host pool directly over PCIe                    */
 #define AEGKV_MODE_STAGED 2 /* gather/scatter kernel <-> contiguous device
-                               staging, plus SDMA hipMemcpyAsync of merged runs */
+                               staging, plus hipMemcpyAsync of merged runs
+                               (the runtime runs them on SDMA engines or as
+                               blit kernels); leaves the CUs to concurrent
+                               compute                                         */
 
 /* Environment, read once per process before the first call:
  *   AEGKV_AUTO_D2H, AEGKV_AUTO_H2D = direct | staged   (what AUTO picks)
