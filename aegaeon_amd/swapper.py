@@ -183,6 +183,7 @@ class KVSwapper:
                 f"groups={len(group_ids)}, first={len(first_kernel_blocks)}, "
                 f"valid={len(valid_kernel_blocks)}"
             )
+        self._require_open()
         groups = np.asarray(group_ids, dtype=np.int64).reshape(-1)
         if groups.size and (groups.min() < 0 or groups.max() >= len(self.group_descriptors)):
             bad = groups[(groups < 0) | (groups >= len(self.group_descriptors))][0]
@@ -278,6 +279,7 @@ class KVSwapper:
         aegkv_migrate_blocks launch; returns the completion event and, with
         fences configured, publishes last_fence for the swap-in word.
         """
+        self._require_open()
         if source_engine_id not in self.peer_caches:
             raise KeyError(f"engine {source_engine_id}'s cache is not registered")
         if len(source_block_ids) != len(target_block_ids):
@@ -312,6 +314,10 @@ class KVSwapper:
                     "source fence that was never signalled; swaps after that wait may have "
                     "read data before its producer wrote it")
 
+    def _require_open(self) -> None:
+        if self.swap_in_stream is None:
+            raise RuntimeError("this KVSwapper is closed")
+
     def close(self) -> None:
         """Wait for this swapper's swaps and release its dedicated streams,
         if it has any (their hardware queues are returned at once). The
@@ -325,9 +331,11 @@ class KVSwapper:
         self.swap_in_stream = self.swap_out_stream = None
 
     def wait_for_all_move_in(self) -> None:
+        self._require_open()
         self.swap_in_stream.synchronize()
         self._check_fences(1, self.swap_in_stream)
 
     def wait_for_all_move_out(self) -> None:
+        self._require_open()
         self.swap_out_stream.synchronize()
         self._check_fences(0, self.swap_out_stream)

@@ -862,7 +862,8 @@ def test_swapper_block_table_round_trip(gpu, oracle, streams):
         assert np.array_equal(t.cpu().numpy().view(np.uint8), w)
     assert ev2.query()
     sw.close()
-    assert sw.swap_in_stream is None
+    with pytest.raises(RuntimeError, match="closed"):
+        sw.wait_for_all_move_in()
     pool.free()
 
 
