@@ -59,7 +59,7 @@ class KVSwapper:
                  fence_words: Optional[torch.Tensor] = None,
                  fence_slots: Optional[Tuple[int, int]] = None,
                  fence_timeout_s: float = 30.0, dedicated_streams: bool = False,
-                 swap_cu_mask: Optional[Sequence[int]] = None):
+                 swap_cu_mask: Optional[Sequence[int]] = None, mode: str = "auto"):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
         if len(group_descriptors) > 64:
@@ -67,6 +67,11 @@ class KVSwapper:
         if not 0 <= tp_rank < tp_size:
             raise ValueError(f"tp_rank {tp_rank} outside [0, {tp_size})")
         self.cache = cache
+        # transfer design for swaps that do not name one: "auto" (the
+        # library's choice, DIRECT), "direct", or "staged" (link traffic on
+        # DMA engines; the mode to use while a model computes beside swaps)
+        ops._mode(mode)
+        self.mode = mode
         self.interprocess_events = interprocess_events
         self.group_descriptors = list(group_descriptors)
         self.tp_rank = tp_rank
@@ -165,7 +170,7 @@ class KVSwapper:
                     first_kernel_blocks: Sequence[int], valid_kernel_blocks: Sequence[int],
                     source_events: Sequence[Optional[Union[torch.cuda.Event, bytes,
                                                            "FenceToken"]]],
-                    is_swap_in: bool, mode="auto") -> torch.cuda.Event:
+                    is_swap_in: bool, mode=None) -> torch.cuda.Event:
         """Move the live extents of some blocks between host and device.
 
         is_swap_in: host block source_block_ids[i] -> device block
@@ -195,8 +200,8 @@ class KVSwapper:
         side = 1 if is_swap_in else 0
         self._wait_sources(request_ids, source_events, stream, side)
         self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
-                          first_kernel_blocks, valid_kernel_blocks, is_swap_in, mode=mode,
-                          stream=stream)
+                          first_kernel_blocks, valid_kernel_blocks, is_swap_in,
+                          mode=self.mode if mode is None else mode, stream=stream)
         self._finish(request_ids, side, stream, new_event)
         if logger.isEnabledFor(logging.INFO):
             valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)

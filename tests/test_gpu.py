@@ -806,12 +806,12 @@ def test_runs_on_current_stream_and_orders_by_events(gpu):
 
 # ------------------------------------------------------------ swapper --
 
-@pytest.mark.parametrize("streams", ["pool", "dedicated", "partitioned"])
+@pytest.mark.parametrize("streams", ["pool", "dedicated", "partitioned", "staged"])
 def test_swapper_block_table_round_trip(gpu, oracle, streams):
     """BlockTable.transfer_entries -> KVSwapper.swap_blocks out and back in,
     partial extents included, checked against the oracle; on torch pool
-    streams, dedicated streams, and dedicated streams on CUs 0-7 of every
-    XCD."""
+    streams, dedicated streams, dedicated streams on CUs 0-7 of every XCD,
+    and with the swapper's default mode set to STAGED."""
     from aegaeon_amd.cache_groups import BlockTable, CacheGroupConfig, CacheGroupRuntimeConfig
     from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
     from aegaeon_amd.swapper import KVSwapper
@@ -829,8 +829,9 @@ def test_swapper_block_table_round_trip(gpu, oracle, streams):
     pool = ops.PinnedHostPool(n_host * cache.page_size_bytes)
     pool.tensor.zero_()
     sw = KVSwapper(cache, [{"full.0", "full.1"}, {"win.0", "win.1"}], descr, pool.tensor,
-                   dedicated_streams=streams != "pool",
-                   swap_cu_mask=ops.xcd_cu_mask(8) if streams == "partitioned" else None)
+                   dedicated_streams=streams not in ("pool", "staged"),
+                   swap_cu_mask=ops.xcd_cu_mask(8) if streams == "partitioned" else None,
+                   mode="staged" if streams == "staged" else "auto")
     table = BlockTable(0, (cache.page_size_bytes // 2,), groups,
                        [[3, 4, 5, 6], [7, 8, 9, 10]])
     tokens = 230
