@@ -95,6 +95,9 @@ extern "C" {
                                         (default 3)                        */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
                                         uncached pool: workgroups (112)    */
+#define AEGKV_TUNE_STAGED_SDMA 16    /* 1: STAGED copies on SDMA engines the
+                                        library drives (two per direction)
+                                        instead of hipMemcpyAsync (0)      */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);
