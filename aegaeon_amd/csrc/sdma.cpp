@@ -415,7 +415,11 @@ struct HostWait {
   const uint64_t* done;
   uint64_t value;
   uint64_t* timed_out;
+  const Lane* lane;
 };
+
+std::mutex g_late_mu;
+std::string g_late;  // what the last wait that ran out of time waited for
 
 void host_wait(void* data) {
   HostWait* w = static_cast<HostWait*>(data);
@@ -425,7 +429,19 @@ void host_wait(void* data) {
       std::this_thread::yield();
       continue;
     }
-    if (std::chrono::steady_clock::now() - t0 > kHostWait) {
+    const auto waited = std::chrono::steady_clock::now() - t0;
+    if (waited > kHostWait) {
+      char buf[200];
+      std::snprintf(buf, sizeof buf,
+                    "a %s wait for job %llu gave up after %.1f s with the done word at %llu",
+                    w->lane->dir == DIR_TO_HOST ? "to-host" : "to-device",
+                    static_cast<unsigned long long>(w->value),
+                    std::chrono::duration<double>(waited).count(),
+                    static_cast<unsigned long long>(__atomic_load_n(w->done, __ATOMIC_ACQUIRE)));
+      {
+        std::lock_guard<std::mutex> lk(g_late_mu);
+        g_late = buf;
+      }
       __atomic_store_n(w->timed_out, uint64_t(1), __ATOMIC_RELEASE);
       break;
     }
@@ -511,7 +527,8 @@ void abandon(const LaneRef& ref, uint64_t seq) {
 
 hipError_t enqueue_wait(const LaneRef& ref, uint64_t seq, uint64_t* timed_out,
                         hipStream_t stream) {
-  auto* w = new HostWait{static_cast<Lane*>(ref.lane)->done, seq, timed_out};
+  const Lane* l = static_cast<const Lane*>(ref.lane);
+  auto* w = new HostWait{l->done, seq, timed_out, l};
   hipError_t e = hipLaunchHostFunc(stream, host_wait, w);
   if (e != hipSuccess) delete w;
   return e;
@@ -524,21 +541,28 @@ std::string describe(int device) {
     for (const auto& kv : g_lanes)
       if (std::get<0>(kv.first) == device) lanes.push_back(kv.second);
   }
-  if (lanes.empty()) return "no SDMA lanes";
   std::string out;
+  {
+    std::lock_guard<std::mutex> lk(g_late_mu);
+    if (!g_late.empty()) out = g_late + "; ";
+  }
+  if (lanes.empty()) return out + "no SDMA lanes";
   for (Lane* lp : lanes) {
     Lane& l = *lp;
     uint64_t submitted, finished;
+    std::string error;
     {
       std::lock_guard<std::mutex> lk(l.mu);
       submitted = l.submitted;
       finished = l.finished;
+      error = l.error;
     }
-    char buf[224];
+    char buf[256];
     std::snprintf(buf, sizeof buf,
-                  "%s%s lane: %s (job %llu; jobs submitted %llu, finished %llu; done word %llu; "
+                  "%s%s lane%s: %s (job %llu; jobs submitted %llu, finished %llu; done word %llu; "
                   "engine %d of mask 0x%x/0x%x has %lld copies pending)",
                   out.empty() ? "" : "; ", l.dir == DIR_TO_HOST ? "to-host" : "to-device",
+                  l.broken.load() ? " (broken)" : "",
                   stage_name(l.stage.load()), static_cast<unsigned long long>(l.current.load()),
                   static_cast<unsigned long long>(submitted),
                   static_cast<unsigned long long>(finished),
@@ -546,6 +570,7 @@ std::string describe(int device) {
                   l.waiting_engine.load(), l.engines[0], l.engines[1],
                   static_cast<long long>(l.pending.load()));
     out += buf;
+    if (!error.empty()) out += " error: " + error;
   }
   return out;
 }

@@ -54,9 +54,6 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
-    p.add_argument("--staged-sdma", action="store_true",
-                   help="STAGED calls put their copies on SDMA engines the library drives "
-                        "(sets the STAGED_SDMA tuning key for the whole run)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-switch", action="store_true",
                    help="skip the model-switch line (both link directions at once)")
@@ -489,7 +486,8 @@ def bench_switch(args):
         free[:] = list(rng.permutation(free))
         # dedicated streams: nothing else runs on the GPU here, and the
         # swap-out and swap-in never land on one hardware queue
-        sw.append(KVSwapper(caches[e], names, descr, host.tensor, dedicated_streams=True))
+        sw.append(KVSwapper(caches[e], names, descr, host.tensor, dedicated_streams=True,
+                            mode=getattr(args, "mode", "auto")))
     tables, reqs = {}, [[], []]
     for e in range(2):
         for i, tok in enumerate(lengths[e]):
@@ -580,9 +578,8 @@ def bench_serving(args):
     contiguous runs, as the slab allocator hands them out. Reported: the
     GEMM's TFLOP/s alone and beside the swaps, and the swap rates, for
     DIRECT with the default swap grid, DIRECT with a smaller grid (24
-    workgroups per direction, 4 loads per lane), STAGED (gather/scatter
-    kernels in HBM, the link crossed by runtime copies) and STAGED with the
-    copies on SDMA engines the library drives."""
+    workgroups per direction, 4 loads per lane) and STAGED (gather/scatter
+    kernels in HBM, the link crossed by runtime copies)."""
     import numpy as np
     import torch
 
@@ -656,10 +653,6 @@ def bench_serving(args):
         _lib.tune(k, v)
     gemm, d2h, h2d = median3(True, "staged")
     out["staged"] = {"gemm_TFLOPs": gemm, "swap_out_GBps": d2h, "swap_in_GBps": h2d}
-    prev_sdma = _lib.tune(_lib.TUNE_STAGED_SDMA, 1)
-    gemm, d2h, h2d = median3(True, "staged")
-    _lib.tune(_lib.TUNE_STAGED_SDMA, prev_sdma)
-    out["staged_sdma"] = {"gemm_TFLOPs": gemm, "swap_out_GBps": d2h, "swap_in_GBps": h2d}
     di, do = torch.from_numpy(in_ids).to(dev), torch.from_numpy(out_ids).to(dev)
     pages = pool.tensor.view(HOST, S, tile)
     ok = all(torch.equal(pages[int(host_ids[k]), s].to(dev),
@@ -872,12 +865,6 @@ def main():
               "(swaps shard per GPU with no exchange step; run one process per GPU).",
               file=sys.stderr)
         sys.exit(2)
-    if args.staged_sdma:
-        import torch  # noqa: F401  (the library binds torch's HIP runtime)
-
-        from aegaeon_amd import _lib
-        _lib.load()
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 1)
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
               "switch": bench_switch, "serving": bench_serving}[args.config]
@@ -1073,9 +1060,7 @@ def main():
     if not args.no_side_by_side:
         log("DIRECT and STAGED side by side, one call at a time")
         side = {}
-        for design in ("direct", "staged", "staged_sdma"):
-            mode = "direct" if design == "direct" else "staged"
-            prev_sdma = _lib.tune(_lib.TUNE_STAGED_SDMA, int(design == "staged_sdma"))
+        for mode in ("direct", "staged"):
             rates = {"d2h": [], "h2d": []}
             for rep in range(4):
                 for name, sargs in (("d2h", (out_ids, host_ids, zero, zero, ones, False)),
@@ -1088,16 +1073,13 @@ def main():
                     b.synchronize()
                     if rep:
                         rates[name].append(swap_bytes / (a.elapsed_time(b) / 1e3) / 1e9)
-            _lib.tune(_lib.TUNE_STAGED_SDMA, prev_sdma)
             if not all(torch.equal(s[di], s[do]) for s in segs1):
-                raise AssertionError(f"{design} side-by-side round trip is not bit-exact")
-            side[design] = {k: round(float(np.median(v)), 3) for k, v in rates.items()}
+                raise AssertionError(f"{mode} side-by-side round trip is not bit-exact")
+            side[mode] = {k: round(float(np.median(v)), 3) for k, v in rates.items()}
         line["designs_side_by_side"] = {
             "what": "same 1024 blocks and pool; median of 3 calls per direction after one "
-                    "warm-up, each call timed alone; staged_sdma = STAGED with the copies on "
-                    "two SDMA engines per direction driven by the library",
-            "direct_GBps": side["direct"], "staged_GBps": side["staged"],
-            "staged_sdma_GBps": side["staged_sdma"]}
+                    "warm-up, each call timed alone",
+            "direct_GBps": side["direct"], "staged_GBps": side["staged"]}
     pool.free()
     del segs1, segs2
     torch.cuda.empty_cache()
@@ -1121,7 +1103,7 @@ def main():
         log("serving: swaps beside a bf16 GEMM loop")
         sv = bench_serving(args)
         line["serving"] = {k: sv[k] for k in ("gemm_alone_TFLOPs", "default_grid", "grid_24x4",
-                                              "staged", "staged_sdma", "bit_exact")}
+                                              "staged", "bit_exact")}
         line["serving"]["workload"] = sv["config"]["workload"]
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:

@@ -97,7 +97,9 @@ extern "C" {
                                         uncached pool: workgroups (112)    */
 #define AEGKV_TUNE_STAGED_SDMA 16    /* 1: STAGED copies on SDMA engines the
                                         library drives (two per direction)
-                                        instead of hipMemcpyAsync (0)      */
+                                        instead of hipMemcpyAsync (0).
+                                        1 is refused for now: the mode is
+                                        switched off                       */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);
