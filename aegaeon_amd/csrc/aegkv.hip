@@ -1483,11 +1483,13 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "staged SDMA is 0 or 1");
     // Switched off: in a run with both directions at once, copies issued
     // on fixed engines with hsa_amd_memory_async_copy_on_engine were still
-    // incomplete after 60 s; the cause is not known.
+    // incomplete after 60 s. ROCr's header warns that this call used
+    // together with hsa_amd_memory_async_copy (which hipMemcpyAsync makes,
+    // with engines the runtime assigns) can cause resource conflicts.
     if (key == AEGKV_TUNE_STAGED_SDMA && value == 1)
       return fail(AEGKV_EINVAL, "STAGED on library-driven SDMA engines is switched off: its "
-                  "copies were left incomplete in a run with both directions at once (cause "
-                  "not known)");
+                  "copies were left incomplete in a run with both directions at once, likely "
+                  "a conflict with the engines the runtime assigns to hipMemcpyAsync");
     if (key == AEGKV_TUNE_STAGED_OVERLAP && value > 3)
       return fail(AEGKV_EINVAL, "staged overlap is a 2-bit mask (0-3)");
     *slot = value;

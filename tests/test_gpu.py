@@ -20,10 +20,12 @@ pytestmark = pytest.mark.gpu
 
 # STAGED with the copies on library-driven SDMA engines is switched off in
 # the library (its tuning value 1 is refused): in a model-switch run with
-# both directions at once its copies were still incomplete after 60 s, and
-# the cause is not known. Its cases stay here, skipped.
+# both directions at once its copies were still incomplete after 60 s,
+# likely a conflict between fixed-engine copies and the engines the runtime
+# assigns to hipMemcpyAsync. Its cases stay here, skipped.
 SDMA_OFF = ("STAGED on library-driven SDMA engines is switched off: copies were left "
-            "incomplete in a two-direction run, cause not known")
+            "incomplete in a two-direction run (likely a conflict with the runtime's own "
+            "engine assignment)")
 
 MODES = ("direct", "staged")
 
