@@ -9,7 +9,6 @@ inverse of the layout, and planted mistakes that these checks must catch.
 """
 
 import math
-import re
 import subprocess
 
 import numpy as np
@@ -311,7 +310,6 @@ MUTANTS = {
 def test_planted_mistake_is_caught(oracle, tmp_path, name, golden):
     """Each mutant of the oracle source must fail the provenance check, the
     golden fixture or the brute-force extent check."""
-    import ctypes
     import importlib
 
     src = oracle.SRC.read_text()
