@@ -289,7 +289,7 @@ def test_copy_blocks_seeded_vs_oracle(gpu, oracle):
     assert np.array_equal(seg.cpu().numpy(), segs_np[4])
 
 
-@pytest.mark.parametrize("case", range(24))
+@pytest.mark.parametrize("case", range(96))
 def test_randomized_block_copies_vs_oracle(gpu, oracle, restore_tuning, case):
     """Random copy_blocks within one cache (1-20 segments of 16 B-multiple
     or odd pages, repeated sources, random kernel shapes, grids, LDS
@@ -547,7 +547,7 @@ def _random_case(rng):
                 grp=grp, first=first, valid=valid)
 
 
-@pytest.mark.parametrize("case", range(40))
+@pytest.mark.parametrize("case", range(160))
 def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     """Random layouts (groups, extents, TP ranks, byte and 16 B paths),
     both modes, random staging chunk sizes, DMA stream counts, overlap
