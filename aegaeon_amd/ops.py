@@ -11,6 +11,7 @@ libaegkv.so; there is no Python or CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import sys
 import weakref
 from typing import Sequence
 
@@ -373,9 +374,13 @@ class _OwnedStream(torch.cuda.ExternalStream):
             _lib.load().aegkv_stream_destroy(ctypes.c_void_p(ptr))
 
     def __del__(self):
+        # At interpreter exit the HIP runtime may already be torn down, and
+        # the process is ending anyway: leave the stream to it.
+        if sys.is_finalizing():
+            return
         try:
             self._aegkv_close()
-        except Exception:  # interpreter shutdown: the process is ending anyway
+        except Exception:
             pass
 
 
