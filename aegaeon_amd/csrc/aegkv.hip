@@ -110,8 +110,9 @@ struct Tunables {
   // swap-out's copies to SDMA and it fell to 29 GB/s (35 one chunk at a
   // time); set bit 0 off for that pattern.
   int64_t staged_overlap = 3;
-  // STAGED copies on SDMA engines the library drives itself (1) instead of
-  // hipMemcpyAsync, where the runtime picks the engine (0).
+  // STAGED copies issued by the library to ROCr's DMA copy call, with
+  // host-function waits (1), instead of hipMemcpyAsync, which the runtime
+  // may run as a CU-holding blit kernel (0).
   int64_t staged_sdma = 0;
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
@@ -1125,7 +1126,7 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
 // flags the wait (the lane's own budget, in sdma.cpp).
 constexpr int64_t kSdmaWaitSeconds = 60;
 
-// STAGED with the copies on SDMA engines the library drives (sdma.cpp):
+// STAGED with the copies issued by the library as DMA copies (sdma.cpp):
 // two staging buffers, chunk c in buffer c % 2, both directions
 // double-buffered. Each chunk's copies are a job of the stream's lane for
 // that direction; the stream releases a job by storing its number into the
@@ -1481,15 +1482,6 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
     if (key == AEGKV_TUNE_STAGED_SDMA && value > 1)
       return fail(AEGKV_EINVAL, "staged SDMA is 0 or 1");
-    // Switched off: in a run with both directions at once, copies issued
-    // on fixed engines with hsa_amd_memory_async_copy_on_engine were still
-    // incomplete after 60 s. ROCr's header warns that this call used
-    // together with hsa_amd_memory_async_copy (which hipMemcpyAsync makes,
-    // with engines the runtime assigns) can cause resource conflicts.
-    if (key == AEGKV_TUNE_STAGED_SDMA && value == 1)
-      return fail(AEGKV_EINVAL, "STAGED on library-driven SDMA engines is switched off: its "
-                  "copies were left incomplete in a run with both directions at once, likely "
-                  "a conflict with the engines the runtime assigns to hipMemcpyAsync");
     if (key == AEGKV_TUNE_STAGED_OVERLAP && value > 3)
       return fail(AEGKV_EINVAL, "staged overlap is a 2-bit mask (0-3)");
     *slot = value;

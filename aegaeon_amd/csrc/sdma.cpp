@@ -1,12 +1,16 @@
-// SDMA engines driven by the library, for STAGED host transfers.
+// DMA-engine copies issued by the library, for STAGED host transfers.
 //
 // STAGED moves each chunk between device staging and the host pool with
-// copies; hipMemcpyAsync leaves the choice of engine (a blit kernel on the
-// stream's queue or an SDMA engine) to the HIP runtime. Here the copies go
-// to fixed SDMA engines through ROCr's public copy-on-engine call
-// (hsa_amd_memory_async_copy_on_engine), two engines per direction, so the
-// link traffic never occupies a CU and its rate does not depend on the
-// runtime's choice.
+// copies. hipMemcpyAsync leaves the choice between an SDMA engine and a
+// blit kernel on the stream's queue to the HIP runtime. A blit kernel holds
+// CUs for the whole copy (under rocprof's kernel trace the runtime ran
+// these copies as 256-workgroup blit kernels, and a GEMM beside them lost
+// half its rate). Here each chunk's copies go straight to ROCr's
+// hsa_amd_memory_async_copy, which runs host<->device copies on the
+// agent's SDMA engines. The engines are the runtime's own choice: ROCr's
+// header warns that fixing engines with hsa_amd_memory_async_copy_on_engine
+// while other code uses hsa_amd_memory_async_copy "can result in resource
+// conflicts", and hipMemcpyAsync is such other code.
 //
 // Ordering with the caller's HIP stream, without any device-side wait and
 // without any HIP call on the library's threads:
@@ -69,8 +73,7 @@ struct Api {
   decltype(&hsa_signal_create) signal_create = nullptr;
   decltype(&hsa_signal_destroy) signal_destroy = nullptr;
   decltype(&hsa_signal_wait_scacquire) signal_wait = nullptr;
-  decltype(&hsa_amd_memory_async_copy_on_engine) copy_on_engine = nullptr;
-  decltype(&hsa_amd_memory_copy_engine_status) engine_status = nullptr;
+  decltype(&hsa_amd_memory_async_copy) async_copy = nullptr;
   uint64_t ticks_per_s = 0;  // unit of the signal waits' timeout hint
 };
 
@@ -110,9 +113,8 @@ int load_api(Api** out) {
       !bind(lib, "hsa_signal_create", &a.signal_create) ||
       !bind(lib, "hsa_signal_destroy", &a.signal_destroy) ||
       !bind(lib, "hsa_signal_wait_scacquire", &a.signal_wait) ||
-      !bind(lib, "hsa_amd_memory_async_copy_on_engine", &a.copy_on_engine) ||
-      !bind(lib, "hsa_amd_memory_copy_engine_status", &a.engine_status))
-    return fail(AEGKV_EINVAL, "the HSA runtime %s lacks the copy-on-engine calls", path.c_str());
+      !bind(lib, "hsa_amd_memory_async_copy", &a.async_copy))
+    return fail(AEGKV_EINVAL, "the HSA runtime %s lacks the calls STAGED needs", path.c_str());
   if (a.init() != HSA_STATUS_SUCCESS) return fail(AEGKV_EINVAL, "hsa_init failed");
   if (a.system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &a.ticks_per_s) !=
           HSA_STATUS_SUCCESS || a.ticks_per_s == 0)
@@ -172,13 +174,12 @@ constexpr uint64_t kStartSlots = 1024;
 
 enum Stage : int { IDLE = 0, WAIT_START = 1, COPYING = 2, FAILED = 3 };
 
-// One direction of one device: its engines, pinned words and worker thread.
+// One direction of one stream: its pinned words and worker thread.
 // The thread calls the HSA runtime only.
 struct Lane {
   int dir = 0, device = -1;
   Api* api = nullptr;
   hsa_agent_t dst_agent{0}, src_agent{0};
-  uint32_t engines[2] = {0, 0};
   uint64_t* done = nullptr;  // pinned: number of the newest finished job
   uint64_t* slots = nullptr; // pinned: kStartSlots start slots, job seq at seq % kStartSlots
   std::mutex mu;
@@ -190,8 +191,7 @@ struct Lane {
   std::string error;                // first failure, reported by the next call
   std::atomic<int> stage{IDLE};
   std::atomic<uint64_t> current{0};
-  std::atomic<int64_t> pending{0};  // copies not yet complete on the engine waited for
-  std::atomic<int> waiting_engine{0};
+  std::atomic<int64_t> pending{0};  // copies of the current job not yet complete
   std::atomic<bool> broken{false};  // copies were left pending: no more jobs run
 
   void run() {
@@ -247,89 +247,57 @@ struct Lane {
     }
     if (job.copies.empty() || broken.load()) return "";
     stage.store(COPYING);
-    hsa_signal_t sig[2] = {{0}, {0}};
-    int64_t per_engine[2] = {0, 0};
-    size_t bytes[2] = {0, 0};
-    for (const Copy& c : job.copies) {  // balance the engines by bytes
-      const int i = bytes[0] <= bytes[1] ? 0 : 1;
-      bytes[i] += c.len;
-      ++per_engine[i];
-    }
+    // One completion signal per job: each copy lowers it by one.
+    const int64_t total = static_cast<int64_t>(job.copies.size());
+    hsa_signal_t sig{0};
+    if (api->signal_create(total, 0, nullptr, &sig) != HSA_STATUS_SUCCESS)
+      return "hsa_signal_create failed";
     std::string err;
-    for (int i = 0; i < 2; ++i)
-      if (per_engine[i] && api->signal_create(per_engine[i], 0, nullptr, &sig[i]) !=
-                               HSA_STATUS_SUCCESS)
-        err = "hsa_signal_create failed";
-    int64_t issued[2] = {0, 0};
-    bytes[0] = bytes[1] = 0;
-    for (size_t k = 0; k < job.copies.size() && err.empty(); ++k) {
-      const Copy& c = job.copies[k];
-      const int i = bytes[0] <= bytes[1] ? 0 : 1;
-      bytes[i] += c.len;
-      hsa_status_t s = api->copy_on_engine(c.dst, dst_agent, c.src, src_agent, c.len, 0, nullptr,
-                                           sig[i], static_cast<hsa_amd_sdma_engine_id_t>(
-                                                       engines[i]), false);
-      if (s != HSA_STATUS_SUCCESS) err = "hsa_amd_memory_async_copy_on_engine failed";
-      else ++issued[i];
+    int64_t issued = 0;
+    for (const Copy& c : job.copies) {
+      if (api->async_copy(c.dst, dst_agent, c.src, src_agent, c.len, 0, nullptr, sig) !=
+          HSA_STATUS_SUCCESS) {
+        err = "hsa_amd_memory_async_copy failed";
+        break;
+      }
+      ++issued;
     }
-    // Each copy lowers its engine's signal by one; wait for the issued ones.
-    // Blocked waits with a 2 ms hint, so that a completion whose interrupt
-    // is missed is still seen within 2 ms.
+    // Wait for the issued copies. Blocked waits with a 2 ms hint, so that a
+    // completion whose interrupt is missed is still seen within 2 ms.
+    const hsa_signal_value_t target = total - issued;
     const uint64_t hint = api->ticks_per_s / 500;
     const auto t0 = std::chrono::steady_clock::now();
-    bool stuck = false;
-    for (int i = 0; i < 2; ++i) {
-      if (!sig[i].handle) continue;
-      const hsa_signal_value_t target = per_engine[i] - issued[i];
-      hsa_signal_value_t v;
-      waiting_engine.store(i);
-      for (;;) {
-        v = api->signal_wait(sig[i], HSA_SIGNAL_CONDITION_LT, target + 1, hint,
-                             HSA_WAIT_STATE_BLOCKED);
-        pending.store(v - target);
-        if (v <= target) break;
-        if (std::chrono::steady_clock::now() - t0 > kHostWait) {
-          stuck = true;
-          break;
-        }
-      }
-      if (stuck) {
-        // the engines may still write: keep the signals, fail the lane
+    hsa_signal_value_t v;
+    for (;;) {
+      v = api->signal_wait(sig, HSA_SIGNAL_CONDITION_LT, target + 1, hint,
+                           HSA_WAIT_STATE_BLOCKED);
+      pending.store(v - target);
+      if (v <= target) break;
+      if (std::chrono::steady_clock::now() - t0 > kHostWait) {
+        // the engines may still write: keep the signal, fail the lane
         broken.store(true);
-        std::snprintf(msg, sizeof msg,
-                      "job %llu: %lld of %zu copies on SDMA engine mask 0x%x still pending "
-                      "after %lld s", static_cast<unsigned long long>(job.seq),
-                      static_cast<long long>(v - target), job.copies.size(), engines[i],
-                      static_cast<long long>(kHostWait.count()));
+        std::snprintf(msg, sizeof msg, "job %llu: %lld of %lld copies still pending after %lld s",
+                      static_cast<unsigned long long>(job.seq), static_cast<long long>(v - target),
+                      static_cast<long long>(total), static_cast<long long>(kHostWait.count()));
         return msg;
       }
-      if (v < 0 && err.empty()) err = "an SDMA copy reported an error";
-      api->signal_destroy(sig[i]);
     }
+    if (v < 0 && err.empty()) err = "a DMA copy reported an error";
+    api->signal_destroy(sig);
     pending.store(0);
     return err;
   }
 };
 
-// A device's HSA agents and the engines each direction uses.
+// A device's HSA agents.
 struct DeviceInfo {
   Api* api = nullptr;
   hsa_agent_t gpu{0}, cpu{0};
-  uint32_t engines[2][2] = {};  // [direction][engine]
 };
 
 std::mutex g_dev_mu;
 std::map<int, DeviceInfo*> g_dev;                                   // lives until exit
 std::map<std::tuple<int, int, uintptr_t>, Lane*> g_lanes;           // lives until exit
-
-uint32_t pick(uint32_t mask, uint32_t avoid, int nth) {
-  int seen = 0;
-  for (int b = 0; b < 32; ++b) {
-    const uint32_t bit = 1u << b;
-    if ((mask & bit) && !(avoid & bit) && seen++ == nth) return bit;
-  }
-  return 0;
-}
 
 // Under g_dev_mu.
 int device_info(int dev, DeviceInfo** out) {
@@ -358,26 +326,10 @@ int device_info(int dev, DeviceInfo** out) {
   if (api->agent_get_info(ag.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
                           &near_cpu) == HSA_STATUS_SUCCESS && near_cpu.handle)
     cpu = near_cpu;
-  uint32_t to_host = 0, to_dev = 0;
-  if (api->engine_status(cpu, ag.gpu, &to_host) != HSA_STATUS_SUCCESS ||
-      api->engine_status(ag.gpu, cpu, &to_dev) != HSA_STATUS_SUCCESS)
-    return fail(AEGKV_EINVAL, "no SDMA engine status for device %d", dev);
-  // two engines per direction, distinct between directions when possible
-  uint32_t out_e0 = pick(to_host, 0, 0), out_e1 = pick(to_host, 0, 1);
-  const uint32_t used = out_e0 | out_e1;
-  uint32_t in_e0 = pick(to_dev, used, 0), in_e1 = pick(to_dev, used, 1);
-  if (!in_e0) in_e0 = pick(to_dev, 0, 0);
-  if (!in_e1) in_e1 = in_e0;
-  if (!out_e1) out_e1 = out_e0;
-  if (!out_e0 || !in_e0) return fail(AEGKV_EINVAL, "device %d reports no free SDMA engine", dev);
   auto* d = new DeviceInfo();
   d->api = api;
   d->gpu = ag.gpu;
   d->cpu = cpu;
-  d->engines[DIR_TO_HOST][0] = out_e0;
-  d->engines[DIR_TO_HOST][1] = out_e1;
-  d->engines[DIR_TO_DEVICE][0] = in_e0;
-  d->engines[DIR_TO_DEVICE][1] = in_e1;
   g_dev[dev] = d;
   *out = d;
   return 0;
@@ -400,8 +352,6 @@ int make_lane(int dev, int dir, DeviceInfo* d, Lane** out) {
   l->api = d->api;
   l->dst_agent = dir == DIR_TO_HOST ? d->cpu : d->gpu;
   l->src_agent = dir == DIR_TO_HOST ? d->gpu : d->cpu;
-  l->engines[0] = d->engines[dir][0];
-  l->engines[1] = d->engines[dir][1];
   l->done = static_cast<uint64_t*>(p);
   l->slots = l->done + 8;
   std::thread([l] { l->run(); }).detach();
@@ -560,14 +510,13 @@ std::string describe(int device) {
     char buf[256];
     std::snprintf(buf, sizeof buf,
                   "%s%s lane%s: %s (job %llu; jobs submitted %llu, finished %llu; done word %llu; "
-                  "engine %d of mask 0x%x/0x%x has %lld copies pending)",
+                  "%lld copies pending)",
                   out.empty() ? "" : "; ", l.dir == DIR_TO_HOST ? "to-host" : "to-device",
                   l.broken.load() ? " (broken)" : "",
                   stage_name(l.stage.load()), static_cast<unsigned long long>(l.current.load()),
                   static_cast<unsigned long long>(submitted),
                   static_cast<unsigned long long>(finished),
                   static_cast<unsigned long long>(__atomic_load_n(l.done, __ATOMIC_ACQUIRE)),
-                  l.waiting_engine.load(), l.engines[0], l.engines[1],
                   static_cast<long long>(l.pending.load()));
     out += buf;
     if (!error.empty()) out += " error: " + error;

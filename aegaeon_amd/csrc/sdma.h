@@ -28,7 +28,7 @@ struct LaneRef {
   uint64_t slot_count;
 };
 
-// Set up the device's engines and the stream's lane on first use. Fails,
+// Set up the device's agents and the stream's lane on first use. Fails,
 // once, with the message of an earlier failed transfer on that lane, and
 // always once copies were left pending.
 int lane_for(int device, int dir, hipStream_t stream, LaneRef* out);

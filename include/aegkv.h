@@ -95,11 +95,11 @@ extern "C" {
                                         (default 3)                        */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
                                         uncached pool: workgroups (112)    */
-#define AEGKV_TUNE_STAGED_SDMA 16    /* 1: STAGED copies on SDMA engines the
-                                        library drives (two per direction)
-                                        instead of hipMemcpyAsync (0).
-                                        1 is refused for now: the mode is
-                                        switched off                       */
+#define AEGKV_TUNE_STAGED_SDMA 16    /* 1: STAGED copies issued by the
+                                        library to the HSA runtime's DMA
+                                        copy (SDMA engines), streams held
+                                        by host functions, no CU waits;
+                                        0: hipMemcpyAsync (default)        */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -18,14 +18,6 @@ from aegaeon_amd import _lib, ops
 
 pytestmark = pytest.mark.gpu
 
-# STAGED with the copies on library-driven SDMA engines is switched off in
-# the library (its tuning value 1 is refused): in a model-switch run with
-# both directions at once its copies were still incomplete after 60 s,
-# likely a conflict between fixed-engine copies and the engines the runtime
-# assigns to hipMemcpyAsync. Its cases stay here, skipped.
-SDMA_OFF = ("STAGED on library-driven SDMA engines is switched off: copies were left "
-            "incomplete in a two-direction run (likely a conflict with the runtime's own "
-            "engine assignment)")
 
 MODES = ("direct", "staged")
 
@@ -423,9 +415,7 @@ def test_swap_kernel_shapes_vs_oracle(gpu, oracle, restore_tuning, shape_auto, u
         pool.free()
 
 
-@pytest.mark.parametrize("dma_streams", [0, 1, 3, 4,
-                                         pytest.param("sdma", marks=pytest.mark.skip(
-                                             reason=SDMA_OFF))])
+@pytest.mark.parametrize("dma_streams", [0, 1, 3, 4, "sdma"])
 def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     """STAGED copies forked over 0-4 library streams, or issued on SDMA
     engines the library drives (and split into small staging chunks), land
@@ -474,10 +464,7 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
 
 @pytest.mark.parametrize("dma_streams,contiguous,overlap",
                          [(2, True, 3), (2, False, 3), (4, False, 3), (2, False, 0),
-                          (1, True, 3),
-                          pytest.param("sdma", True, 3, marks=pytest.mark.skip(reason=SDMA_OFF)),
-                          pytest.param("sdma", False, 3,
-                                       marks=pytest.mark.skip(reason=SDMA_OFF))])
+                          (1, True, 3), ("sdma", True, 3), ("sdma", False, 3)])
 def test_staged_chunked_round_trip(gpu, restore_tuning, dma_streams, contiguous, overlap):
     """STAGED over library streams with two staging buffers in flight (the
     gather or scatter of one chunk beside the copies of another), one chunk
@@ -559,8 +546,7 @@ def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     _lib.tune(_lib.TUNE_STAGING_BYTES, int(rng.choice([1 << 20, 3 << 20, 512 << 20])))
     _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, int(rng.choice([0, 1, 2, 4])))
     _lib.tune(_lib.TUNE_STAGED_OVERLAP, int(rng.integers(0, 4)))
-    rng.integers(0, 2)   # drawn as when it chose STAGED_SDMA, so every case keeps its shape
-    _lib.tune(_lib.TUNE_STAGED_SDMA, 0)
+    _lib.tune(_lib.TUNE_STAGED_SDMA, int(rng.integers(0, 2)))
     shift = int(rng.choice([0, 0, 16, 1]))
     page, kpp, n = c["page"], c["kpp"], c["n"]
     composite = int(page.sum())
@@ -595,7 +581,7 @@ def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     raw.free()
 
 
-@pytest.mark.parametrize("sdma", [0, pytest.param(1, marks=pytest.mark.skip(reason=SDMA_OFF))])
+@pytest.mark.parametrize("sdma", [0, 1])
 def test_staged_swap_out_and_in_at_once(gpu, restore_tuning, sdma):
     """A STAGED swap-out and a STAGED swap-in enqueued together on two
     streams, each double-buffered over its own DMA streams with 8 MiB

@@ -325,9 +325,8 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_STAGED_SDMA) == 0
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_STAGED_SDMA, 2)
-    with pytest.raises(ValueError, match="switched off"):
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 1)
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA) == 0
+    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 1) == 0
+    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 0) == 1
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):
