@@ -111,8 +111,8 @@ struct Tunables {
   // time); set bit 0 off for that pattern.
   int64_t staged_overlap = 3;
   // STAGED copies issued by the library to ROCr's DMA copy call, with
-  // host-function waits (1), instead of hipMemcpyAsync, which the runtime
-  // may run as a CU-holding blit kernel (0).
+  // host-function waits, instead of hipMemcpyAsync, which the runtime may
+  // run as a CU-holding blit kernel: bit 0 for swap-out, bit 1 for swap-in.
   int64_t staged_sdma = 0;
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
@@ -1294,7 +1294,7 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   // Staging comes from hipMallocAsync (256 B aligned) with a composite stride.
   const bool vec_stage = dev_vec && composite % 16 == 0;
   const int k = static_cast<int>(std::min<int64_t>(t.staged_dma_streams, kMaxDmaStreams));
-  if (t.staged_sdma)
+  if ((t.staged_sdma >> (is_swap_in ? 1 : 0)) & 1)
     return staged_sdma(ctx, L, E, order, is_swap_in, composite, step, vec_stage, t, stream);
   const bool overlap = (t.staged_overlap >> (is_swap_in ? 1 : 0)) & 1;
   if (k <= 1 || !overlap)
@@ -1480,8 +1480,8 @@ int64_t aegkv_tune(int key, int64_t value) {
                   static_cast<long long>(kMaxLdsPerWorkgroup));
     if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
-    if (key == AEGKV_TUNE_STAGED_SDMA && value > 1)
-      return fail(AEGKV_EINVAL, "staged SDMA is 0 or 1");
+    if (key == AEGKV_TUNE_STAGED_SDMA && value > 3)
+      return fail(AEGKV_EINVAL, "staged DMA lanes are a 2-bit mask (0-3)");
     if (key == AEGKV_TUNE_STAGED_OVERLAP && value > 3)
       return fail(AEGKV_EINVAL, "staged overlap is a 2-bit mask (0-3)");
     *slot = value;

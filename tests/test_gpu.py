@@ -422,7 +422,7 @@ def test_staged_dma_fanout_vs_oracle(gpu, oracle, restore_tuning, dma_streams):
     exactly where the oracle puts them, both ways."""
     sdma = dma_streams == "sdma"
     dma_streams = 2 if sdma else dma_streams
-    _lib.tune(_lib.TUNE_STAGED_SDMA, int(sdma))
+    _lib.tune(_lib.TUNE_STAGED_SDMA, 3 if sdma else 0)
     _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, dma_streams)
     _lib.tune(_lib.TUNE_STAGING_BYTES, 1 << 20)
     _lib.tune(_lib.TUNE_STAGED_WORKGROUPS, (0, 3, 64, 1)[dma_streams % 4])
@@ -472,7 +472,7 @@ def test_staged_chunked_round_trip(gpu, restore_tuning, dma_streams, contiguous,
     pages, 200 blocks pass through 67 chunks each way, so each buffer is
     reused many times. Host pages must equal the device tiles they came
     from and the round trip must be exact."""
-    _lib.tune(_lib.TUNE_STAGED_SDMA, int(dma_streams == "sdma"))
+    _lib.tune(_lib.TUNE_STAGED_SDMA, 3 if dma_streams == "sdma" else 0)
     _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, 2 if dma_streams == "sdma" else dma_streams)
     _lib.tune(_lib.TUNE_STAGING_BYTES, 8 << 20)
     _lib.tune(_lib.TUNE_STAGED_OVERLAP, overlap)
@@ -546,7 +546,7 @@ def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     _lib.tune(_lib.TUNE_STAGING_BYTES, int(rng.choice([1 << 20, 3 << 20, 512 << 20])))
     _lib.tune(_lib.TUNE_STAGED_DMA_STREAMS, int(rng.choice([0, 1, 2, 4])))
     _lib.tune(_lib.TUNE_STAGED_OVERLAP, int(rng.integers(0, 4)))
-    _lib.tune(_lib.TUNE_STAGED_SDMA, int(rng.integers(0, 2)))
+    _lib.tune(_lib.TUNE_STAGED_SDMA, 3 * int(rng.integers(0, 2)))
     shift = int(rng.choice([0, 0, 16, 1]))
     page, kpp, n = c["page"], c["kpp"], c["n"]
     composite = int(page.sum())
@@ -581,7 +581,7 @@ def test_randomized_swaps_vs_oracle(gpu, oracle, restore_tuning, case):
     raw.free()
 
 
-@pytest.mark.parametrize("sdma", [0, 1])
+@pytest.mark.parametrize("sdma", [0, 1, 2, 3])
 def test_staged_swap_out_and_in_at_once(gpu, restore_tuning, sdma):
     """A STAGED swap-out and a STAGED swap-in enqueued together on two
     streams, each double-buffered over its own DMA streams with 8 MiB

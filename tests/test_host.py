@@ -324,9 +324,9 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 112
     assert _lib.tune(_lib.TUNE_STAGED_SDMA) == 0
     with pytest.raises(ValueError):
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 2)
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 1) == 0
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 0) == 1
+        _lib.tune(_lib.TUNE_STAGED_SDMA, 4)
+    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 2) == 0
+    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 0) == 2
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):
