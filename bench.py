@@ -873,7 +873,7 @@ def main():
 
         from aegaeon_amd import _lib
         _lib.load()
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 1)
+        _lib.tune(_lib.TUNE_STAGED_SDMA, 3)   # both directions
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
               "switch": bench_switch, "serving": bench_serving}[args.config]
