@@ -46,7 +46,6 @@ TUNE_SWAP_UNROLL = 12
 TUNE_STAGED_WORKGROUPS = 13
 TUNE_STAGED_OVERLAP = 14
 TUNE_SWAP_OUT_WORKGROUPS_UNCACHED = 15
-TUNE_STAGED_SDMA = 16
 HOST_UNCACHED = 1
 
 #: every symbol include/aegkv.h declares

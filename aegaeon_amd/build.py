@@ -39,7 +39,7 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile csrc/aegkv.hip, csrc/fence.hip, csrc/plan.cpp and csrc/sdma.cpp into
+    """Compile csrc/aegkv.hip, csrc/fence.hip and csrc/plan.cpp into
     aegaeon_amd/libaegkv.so (always rebuilds)."""
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [
@@ -49,8 +49,6 @@ def build(verbose: bool = False) -> Path:
         str(CSRC / "aegkv.hip"),
         str(CSRC / "fence.hip"),
         str(CSRC / "plan.cpp"),
-        str(CSRC / "sdma.cpp"),
-        "-ldl",
         "-o",
         str(tmp),
     ]

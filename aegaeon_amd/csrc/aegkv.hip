@@ -28,8 +28,6 @@
 #include <hip/hip_runtime.h>
 #include "aegkv.h"
 #include "errors.h"
-#include "fence.h"
-#include "sdma.h"
 
 #include <algorithm>
 #include <cstdarg>
@@ -110,10 +108,6 @@ struct Tunables {
   // swap-out's copies to SDMA and it fell to 29 GB/s (35 one chunk at a
   // time); set bit 0 off for that pattern.
   int64_t staged_overlap = 3;
-  // STAGED copies issued by the library to ROCr's DMA copy call, with
-  // host-function waits, instead of hipMemcpyAsync, which the runtime may
-  // run as a CU-holding blit kernel: bit 0 for swap-out, bit 1 for swap-in.
-  int64_t staged_sdma = 0;
   // copy_blocks, 1024-lane shapes with items of >= 32 KiB: LDS reserved per
   // workgroup so that one workgroup holds a CU (HBM copy rate +1-5 % on
   // 32-160 KiB tiles; 16 KiB items lose 14 % at one per CU, so they keep 0).
@@ -385,8 +379,6 @@ struct DeviceCtx {
     hipEvent_t join_ev[2][kMaxDmaStreams] = {};  // copies done, per staging buffer
     hipEvent_t kernel_ev[2] = {};                // gather / scatter done, per staging buffer
   } dma[2];
-  // pinned word the SDMA-staged waits set when one ran out of time
-  uint64_t* sdma_timed_out = nullptr;
 };
 
 std::mutex g_ctx_mu;
@@ -732,18 +724,16 @@ int validate_layout(const SwapLayout& L, int64_t* composite_bytes, bool* dev_vec
 }
 
 // Pointer checks through the HIP runtime: every segment lies inside one
-// device allocation; in DIRECT mode the host pool is pinned and mapped.
-int check_layout_pointers(const SwapLayout& L, bool direct) {
+// device allocation, and the host pool is pinned and mapped in both modes
+// (DIRECT kernels dereference it; STAGED copies of a pageable pool would be
+// staged again by the runtime, so they are refused too).
+int check_layout_pointers(const SwapLayout& L) {
   for (int32_t s = 0; s < L.num_segments; ++s) {
     int rc = check_device_range(L.bases[s], L.device_num_blocks * L.page_bytes[s],
                                 "segment base");
     if (rc) return rc;
   }
-  if (direct) {
-    int rc = check_host_range(L.host_pool, L.host_num_blocks * L.host_page_bytes, "host_pool");
-    if (rc) return rc;
-  }
-  return 0;
+  return check_host_range(L.host_pool, L.host_num_blocks * L.host_page_bytes, "host_pool");
 }
 
 int validate_list(const SwapLayout& L, const SwapList& E, bool is_swap_in) {
@@ -1122,134 +1112,6 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   return 0;
 }
 
-// Longest a stream waits for a chunk's SDMA copies before it goes on and
-// flags the wait (the lane's own budget, in sdma.cpp).
-constexpr int64_t kSdmaWaitSeconds = 60;
-
-// STAGED with the copies issued by the library as DMA copies (sdma.cpp):
-// two staging buffers, chunk c in buffer c % 2, both directions
-// double-buffered. Each chunk's copies are a job of the stream's lane for
-// that direction; the stream releases a job by storing its number into the
-// job's start slot (a one-wave kernel) and waits for it with a host
-// function, which holds the stream in the command processor and takes no
-// CU from kernels running beside it (a wait kernel would: a bf16 GEMM loop
-// beside two waiting streams ran 37 % slower). Swap-out: wait for the
-// copies of chunk c-2 (buffer reuse), gather chunk c, release its copies;
-// at the end wait for the last copies. Swap-in: release chunks 0 and 1 at
-// once; for each chunk wait for its copies, scatter it, then release chunk
-// c+2 into the buffer just scattered.
-int staged_sdma(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
-                const std::vector<int64_t>& order, bool is_swap_in, int64_t composite,
-                size_t step, bool vec_stage, const Tunables& t, hipStream_t stream) {
-  const int dir = is_swap_in ? aegkv_sdma::DIR_TO_DEVICE : aegkv_sdma::DIR_TO_HOST;
-  aegkv_sdma::LaneRef lane{};
-  int rc = aegkv_sdma::lane_for(ctx->device, dir, stream, &lane);
-  if (rc) return rc;
-  {
-    std::lock_guard<std::mutex> lk(ctx->mu);
-    if (!ctx->sdma_timed_out) {
-      void* p = nullptr;
-      AEGKV_HIP(hipHostMalloc(&p, 64, hipHostMallocMapped | hipHostMallocPortable |
-                                          hipHostMallocCoherent));
-      ctx->sdma_timed_out = static_cast<uint64_t*>(p);
-      *ctx->sdma_timed_out = 0;
-    }
-  }
-  uint64_t* flag = ctx->sdma_timed_out;
-  if (__atomic_exchange_n(flag, uint64_t(0), __ATOMIC_ACQ_REL))
-    return fail(AEGKV_EINVAL, "an earlier SDMA-staged call waited %lld s for its copies and "
-                "went on without them; now: %s",
-                static_cast<long long>(kSdmaWaitSeconds),
-                aegkv_sdma::describe(ctx->device).c_str());
-  const size_t n = order.size();
-  const size_t chunks = (n + step - 1) / step;
-  const int nbuf = chunks > 1 ? 2 : 1;
-  const size_t buf_bytes = std::min(step, n) * static_cast<size_t>(composite);
-  char* buf[2] = {nullptr, nullptr};
-  for (int b = 0; b < nbuf; ++b) {
-    void* p = nullptr;
-    hipError_t e = hipMallocAsync(&p, buf_bytes, stream);
-    if (e != hipSuccess) {
-      if (b) (void)hipFreeAsync(buf[0], stream);
-      return hip_fail(e, "hipMallocAsync(staging)");
-    }
-    buf[b] = static_cast<char*>(p);
-  }
-  uint64_t last = 0;  // newest submitted job
-  // On a failure: wait for the jobs already submitted, then free.
-  auto unwind = [&](int status) {
-    if (last) (void)aegkv_sdma::enqueue_wait(lane, last, flag, stream);
-    for (int b = 0; b < nbuf; ++b) (void)hipFreeAsync(buf[b], stream);
-    (void)hipGetLastError();
-    return status;
-  };
-  std::vector<uint64_t> seq(chunks, 0);
-  std::vector<Run> runs;
-  aegkv_sdma::CopyList copies;
-  // Build chunk c's copies, queue them on the lane and release them at the
-  // stream's current position.
-  auto release = [&](size_t c) -> int {
-    const size_t lo = c * step, hi = std::min(n, lo + step);
-    char* stage = buf[c & 1];
-    runs.clear();
-    for (size_t j = lo; j < hi; ++j)
-      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
-    copies.clear();
-    for (const Run& r : runs) {
-      char* h = L.host_pool + r.host_off;
-      char* st = stage + r.stage_off;
-      copies.push_back(is_swap_in ? aegkv_sdma::CopyRun{st, h, static_cast<size_t>(r.len)}
-                                  : aegkv_sdma::CopyRun{h, st, static_cast<size_t>(r.len)});
-    }
-    int r = aegkv_sdma::submit(lane, copies, &seq[c]);
-    if (r) return r;
-    last = seq[c];
-    hipError_t e = aegkv_enqueue_word_store(lane.slots + seq[c] % lane.slot_count, seq[c], stream);
-    if (e != hipSuccess) {
-      aegkv_sdma::abandon(lane, seq[c]);
-      return hip_fail(e, "start store");
-    }
-    return 0;
-  };
-  auto chunk_runs = [&](size_t c) {
-    const size_t lo = c * step, hi = std::min(n, lo + step);
-    runs.clear();
-    for (size_t j = lo; j < hi; ++j)
-      entry_runs(L, E, order[j], is_swap_in, static_cast<int64_t>(j - lo), composite, runs);
-    return runs.size();
-  };
-  hipError_t e = hipSuccess;
-  if (!is_swap_in) {
-    for (size_t c = 0; c < chunks; ++c) {
-      const size_t lo = c * step, hi = std::min(n, lo + step);
-      if (c >= 2 && (e = aegkv_sdma::enqueue_wait(lane, seq[c - 2], flag, stream)) != hipSuccess)
-        return unwind(hip_fail(e, "counter wait (staging reuse)"));
-      rc = staged_kernel(ctx, L, E, order, lo, hi, false, buf[c & 1], composite, vec_stage,
-                         chunk_runs(c), t, stream);
-      if (rc) return unwind(rc);
-      if ((rc = release(c))) return unwind(rc);
-    }
-    if ((e = aegkv_sdma::enqueue_wait(lane, last, flag, stream)) !=
-        hipSuccess)
-      return unwind(hip_fail(e, "counter wait (last copies)"));
-  } else {
-    for (size_t c = 0; c < std::min<size_t>(2, chunks); ++c)
-      if ((rc = release(c))) return unwind(rc);
-    for (size_t c = 0; c < chunks; ++c) {
-      const size_t lo = c * step, hi = std::min(n, lo + step);
-      if ((e = aegkv_sdma::enqueue_wait(lane, seq[c], flag, stream)) !=
-          hipSuccess)
-        return unwind(hip_fail(e, "counter wait (chunk copies)"));
-      rc = staged_kernel(ctx, L, E, order, lo, hi, true, buf[c & 1], composite, vec_stage,
-                         chunk_runs(c), t, stream);
-      if (rc) return unwind(rc);
-      if (c + 2 < chunks && (rc = release(c + 2))) return unwind(rc);
-    }
-  }
-  for (int b = 0; b < nbuf; ++b) AEGKV_HIP(hipFreeAsync(buf[b], stream));
-  return 0;
-}
-
 int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
               hipStream_t stream) {
   if (mode < AEGKV_MODE_AUTO || mode > AEGKV_MODE_STAGED)
@@ -1265,7 +1127,7 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   rc = validate_list(L, E, is_swap_in);
   if (rc) return rc;
   if (E.n == 0) return 0;
-  rc = check_layout_pointers(L, !staged);
+  rc = check_layout_pointers(L);
   if (rc) return rc;
   DeviceCtx* ctx = nullptr;
   rc = get_ctx(&ctx);
@@ -1294,8 +1156,6 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   // Staging comes from hipMallocAsync (256 B aligned) with a composite stride.
   const bool vec_stage = dev_vec && composite % 16 == 0;
   const int k = static_cast<int>(std::min<int64_t>(t.staged_dma_streams, kMaxDmaStreams));
-  if ((t.staged_sdma >> (is_swap_in ? 1 : 0)) & 1)
-    return staged_sdma(ctx, L, E, order, is_swap_in, composite, step, vec_stage, t, stream);
   const bool overlap = (t.staged_overlap >> (is_swap_in ? 1 : 0)) & 1;
   if (k <= 1 || !overlap)
     return staged_serial(ctx, L, E, order, is_swap_in, composite, step, vec_stage, t, k,
@@ -1451,7 +1311,6 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_COPY_LDS_BYTES: slot = &g_tune.copy_lds_bytes; break;
     case AEGKV_TUNE_STAGED_OVERLAP: slot = &g_tune.staged_overlap; break;
     case AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED: slot = &g_tune.swap_out_workgroups_uncached; break;
-    case AEGKV_TUNE_STAGED_SDMA: slot = &g_tune.staged_sdma; break;
     default: return fail(AEGKV_EINVAL, "unknown tuning key %d", key);
   }
   const int64_t prev = *slot;
@@ -1480,8 +1339,6 @@ int64_t aegkv_tune(int key, int64_t value) {
                   static_cast<long long>(kMaxLdsPerWorkgroup));
     if (key == AEGKV_TUNE_SWAP_SHAPE_AUTO && value > 1)
       return fail(AEGKV_EINVAL, "swap shape selector is 0 or 1");
-    if (key == AEGKV_TUNE_STAGED_SDMA && value > 3)
-      return fail(AEGKV_EINVAL, "staged DMA lanes are a 2-bit mask (0-3)");
     if (key == AEGKV_TUNE_STAGED_OVERLAP && value > 3)
       return fail(AEGKV_EINVAL, "staged overlap is a 2-bit mask (0-3)");
     *slot = value;

@@ -26,7 +26,6 @@
 #include <hip/hip_runtime.h>
 #include "aegkv.h"
 #include "errors.h"
-#include "fence.h"
 
 #include <cstdint>
 #include <mutex>
@@ -53,13 +52,6 @@ constexpr int64_t kMaxWaitMicros = int64_t(600) * 1000 * 1000;
 __global__ void __launch_bounds__(64) fence_signal_kernel(uint64_t* word, uint64_t value) {
   if (threadIdx.x == 0)
     (void)__hip_atomic_fetch_max(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// One writer per word: a plain store, for words in pinned host memory where
-// an atomic read-modify-write would need PCIe atomics.
-__global__ void __launch_bounds__(64) fence_store_kernel(uint64_t* word, uint64_t value) {
-  if (threadIdx.x == 0)
-    __hip_atomic_store(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __global__ void __launch_bounds__(64) fence_wait_kernel(const uint64_t* word, uint64_t value,
@@ -115,11 +107,6 @@ int wall_clock_khz(int64_t* out) {
 }
 
 }  // namespace
-
-hipError_t aegkv_enqueue_word_store(uint64_t* word, uint64_t value, hipStream_t stream) {
-  hipLaunchKernelGGL(fence_store_kernel, dim3(1), dim3(64), 0, stream, word, value);
-  return hipGetLastError();
-}
 
 extern "C" {
 

@@ -54,9 +54,6 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=2)
     p.add_argument("--mode", default="auto", choices=["auto", "direct", "staged"])
-    p.add_argument("--staged-sdma", action="store_true",
-                   help="STAGED calls issue their copies through the library's DMA lanes "
-                        "(sets the STAGED_SDMA tuning key for the whole run)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-switch", action="store_true",
                    help="skip the model-switch line (both link directions at once)")
@@ -868,12 +865,6 @@ def main():
               "(swaps shard per GPU with no exchange step; run one process per GPU).",
               file=sys.stderr)
         sys.exit(2)
-    if args.staged_sdma:
-        import torch  # noqa: F401  (the library binds torch's HIP runtime)
-
-        from aegaeon_amd import _lib
-        _lib.load()
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 3)   # both directions
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
               "switch": bench_switch, "serving": bench_serving}[args.config]

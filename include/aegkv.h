@@ -95,13 +95,7 @@ extern "C" {
                                         (default 3)                        */
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
                                         uncached pool: workgroups (112)    */
-#define AEGKV_TUNE_STAGED_SDMA 16    /* STAGED copies issued by the
-                                        library to the HSA runtime's DMA
-                                        copy (SDMA engines), streams held
-                                        by host functions, no CU waits,
-                                        instead of hipMemcpyAsync: bit 0
-                                        for swap-out, bit 1 for swap-in
-                                        (default 0)                        */
+/* key 16 is retired: aegkv_tune rejects it as an unknown key */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

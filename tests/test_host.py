@@ -322,11 +322,8 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
     assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 3
     assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 112
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA) == 0
-    with pytest.raises(ValueError):
-        _lib.tune(_lib.TUNE_STAGED_SDMA, 4)
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 2) == 0
-    assert _lib.tune(_lib.TUNE_STAGED_SDMA, 0) == 2
+    with pytest.raises(ValueError, match="unknown tuning key 16"):
+        _lib.tune(16)          # the retired library-driven DMA key
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):

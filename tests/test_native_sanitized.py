@@ -52,7 +52,7 @@ def test_library_host_code_under_asan(tmp_path):
     cmd = [lib_build.hipcc(), *lib_build.HIPCC_FLAGS, "-O1", "-g",
            "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
            "-shared-libasan", f"-I{REPO / 'include'}", str(csrc / "aegkv.hip"),
-           str(csrc / "fence.hip"), str(csrc / "plan.cpp"), str(csrc / "sdma.cpp"), "-ldl",
+           str(csrc / "fence.hip"), str(csrc / "plan.cpp"),
            "-o", str(so)]
     res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert res.returncode == 0, res.stderr
