@@ -110,20 +110,79 @@ def _table():
                       group_blocks=[[5, 6, 7, 8], [9, 10, 11, 12], [13]])
 
 
-def test_transfer_entries_brute_force(oracle):
+def transfer_rows_by_enumeration(groups, group_blocks, t):
+    """Rows transfer_entries must give, from token visibility alone
+    (block_manager.py:446-478 over :205-266 and cache_transfer.py:31-94):
+    the next query sits at position t and sees every committed position
+    (p < t) under full attention, the w-1 most recent ones under a window w.
+    A column is dropped when it was released (-1) or when all of its
+    positions are committed and invisible; a kept attention column's extent
+    is the span of kernel blocks holding visible positions ((0, 0) when it
+    holds none); a state page moves whole as (0, 1)."""
+    rows = []
+    for g, (grp, cols) in enumerate(zip(groups, group_blocks)):
+        for c, block in enumerate(cols):
+            if block == -1:
+                continue
+            if grp.kind == "mamba_none":
+                rows.append((g, c, block, 0, 1))
+                continue
+            w = grp.sliding_window
+            page = range(c * grp.block_size, (c + 1) * grp.block_size)
+            visible = [p for p in page if p < t and (w is None or t - p < w)]
+            if not visible and all(p < t for p in page):
+                continue   # wholly committed and invisible: released by the window
+            kbs = {(p - page.start) // grp.kernel_block_size for p in visible}
+            rows.append((g, c, block, min(kbs), max(kbs) - min(kbs) + 1) if kbs
+                        else (g, c, block, 0, 0))
+    return rows
+
+
+def test_transfer_entries_brute_force():
     """Every retained page, with its live kernel-block extent; pages wholly
     before the window are skipped; the mamba page moves whole."""
     t = 100
-    rows = _table().transfer_entries(t)
-    want = []
-    for col in range(4):
-        want.append((0, col, 5 + col) + oracle.kernel_block_extent(t, col, 32, 16))
-    skipped = max(0, t - 20 + 1) // 32
-    for col in range(skipped, 4):
-        want.append((1, col, 9 + col) + oracle.kernel_block_extent(t, col, 32, 16, 20))
-    want.append((2, 0, 13, 0, 1))
-    assert rows == want
-    assert skipped == 2
+    tab = _table()
+    rows = tab.transfer_entries(t)
+    assert rows == transfer_rows_by_enumeration(tab.cache_groups, tab.group_blocks, t)
+    # window 20 at position 100 sees 81..100: columns 0 and 1 of group 1 go
+    assert [r[1] for r in rows if r[0] == 1] == [2, 3]
+
+
+def test_transfer_entries_random_tables_by_enumeration(aegkv_lib):
+    """Random groups (page sizes, kernel blocks per page, windows 1..70),
+    random released columns and token counts: the Python BlockTable and the
+    native planner both give the enumerated rows."""
+    import numpy as np
+
+    from aegaeon_amd.planner import native_transfer_entries
+
+    rng = np.random.default_rng(123)
+    for _ in range(60):
+        groups = []
+        for _g in range(int(rng.integers(1, 4))):
+            kbs = int(rng.choice([1, 2, 4, 8]))
+            bs = kbs * int(rng.choice([1, 2, 3, 4]))
+            w = None if rng.random() < 0.3 else int(rng.integers(1, 71))
+            groups.append(CacheGroupConfig("attention", bs, kbs, sliding_window=w))
+        if rng.random() < 0.3:
+            groups.append(CacheGroupConfig("mamba_none", 1, 1))
+        tables = []
+        for _t in range(4):
+            t = int(rng.integers(0, 120))
+            cols = []
+            for grp in groups:
+                n = 1 if grp.kind == "mamba_none" else -(-(t + 1) // grp.block_size)
+                ids = rng.integers(1, 1000, n)
+                ids[rng.random(n) < 0.15] = -1
+                cols.append([int(x) for x in ids])
+            tables.append((BlockTable(location=0, block_shape=(8,), cache_groups=tuple(groups),
+                                      group_blocks=cols), t))
+        native = native_transfer_entries(groups, tables)
+        for (tab, t), nat in zip(tables, native):
+            want = transfer_rows_by_enumeration(groups, tab.group_blocks, t)
+            assert tab.transfer_entries(t) == want, (groups, tab.group_blocks, t)
+            assert nat == want, (groups, tab.group_blocks, t)
 
 
 def test_moved_tables_and_metadata():

@@ -67,14 +67,33 @@ def test_byte_extent_and_prefix(oracle):
         oracle.prefix_bytes_for_kernel_blocks(384, 4, 5)
 
 
-def test_window_helpers_brute_force(oracle):
+def visible_to_next_query(p: int, t: int, w) -> bool:
+    """Whether committed token position p (< t) is visible to the next query,
+    which sits at absolute position t: every earlier position for full
+    attention (w None), the w-1 most recent ones under a sliding window of w
+    (the window counts the query itself; block_manager.py:205-213)."""
+    return p < t and (w is None or t - p < w)
+
+
+def skipped_pages_by_enumeration(t: int, bs: int, w: int) -> int:
+    """Leading pages of bs positions none of whose positions the next query
+    can see and all of whose positions are committed: the pages a sliding
+    window of w lets the cache release (cache_transfer.py:31-45,
+    'leading complete pages invisible to the next SW query')."""
+    n = 0
+    while all(p < t and not visible_to_next_query(p, t, w)
+              for p in range(n * bs, (n + 1) * bs)):
+        n += 1
+    return n
+
+
+def check_window_helpers(oracle):
     for bs in (1, 4, 16):
         for w in (1, 2, 5, 16, 33):
             for t in range(0, 120):
                 assert oracle.logical_blocks_for_tokens(t, bs) == math.ceil(t / bs)
-                # pages wholly below the window's first live token
-                live_lo = max(0, t - w + 1)
-                assert oracle.num_skipped_sliding_window_blocks(t, bs, w) == live_lo // bs
+                assert oracle.num_skipped_sliding_window_blocks(t, bs, w) == \
+                    skipped_pages_by_enumeration(t, bs, w), (t, bs, w)
                 # worst case over a query landing anywhere: pages a W-1 token
                 # history plus the current page can touch
                 worst = 0
@@ -83,6 +102,25 @@ def test_window_helpers_brute_force(oracle):
                     worst = max(worst, len({p // bs for p in span}))
                 want = min(math.ceil(t / bs), worst) if t else 0
                 assert oracle.sliding_window_resident_block_bound(t, bs, w) == want
+
+
+def test_window_helpers_brute_force(oracle):
+    check_window_helpers(oracle)
+
+
+def test_skip_rule_known_answers(oracle):
+    """Hand-worked cases of the release rule. 100 committed tokens, 32-token
+    pages, window 20: the next query (position 100) sees 81..100, so pages
+    0 (0-31) and 1 (32-63) are invisible and page 2 (64-95) is not. A
+    window of 1 sees only the query: every complete committed page goes.
+    A window one token short of reaching a page keeps it."""
+    assert oracle.num_skipped_sliding_window_blocks(100, 32, 20) == 2
+    assert oracle.num_skipped_sliding_window_blocks(96, 32, 1) == 3
+    assert oracle.num_skipped_sliding_window_blocks(95, 32, 1) == 2    # page 2 holds 64-94
+    assert oracle.num_skipped_sliding_window_blocks(64, 32, 1) == 2
+    assert oracle.num_skipped_sliding_window_blocks(64, 32, 2) == 1    # sees 63
+    assert oracle.num_skipped_sliding_window_blocks(0, 16, 5) == 0
+    assert oracle.num_skipped_sliding_window_blocks(10, 16, 100) == 0
 
 
 def test_reference_benchmark_extent_plan(oracle):
@@ -303,6 +341,12 @@ MUTANTS = {
     # off-by-one at the window's first live token
     "window_off_by_one": ("live_start = cached_tokens - sliding_window + 1;",
                           "live_start = cached_tokens - sliding_window;"),
+    # count a partly visible page as released (ceil instead of floor)
+    "skip_rounds_up": ("*out = skipped / block_size;",
+                       "*out = (skipped + block_size - 1) / block_size;"),
+    # drop the query's own slot from the window in the release rule
+    "skip_window_off_by_one": ("skipped = processed_computed_tokens - sliding_window + 1;",
+                               "skipped = processed_computed_tokens - sliding_window;"),
 }
 
 
@@ -339,6 +383,11 @@ def test_planted_mistake_is_caught(oracle, tmp_path, name, golden):
         if not caught:
             try:
                 test_extent_matches_golden_brute_force(mod, golden)
+            except AssertionError:
+                caught = True
+        if not caught:
+            try:
+                check_window_helpers(mod)
             except AssertionError:
                 caught = True
         assert caught, f"mutant {name} survived"
