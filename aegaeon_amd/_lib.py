@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must precede loading libaegkv, see module doc)
 
 LIB_PATH = Path(__file__).resolve().parent / "libaegkv.so"
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 EINVAL = -1
@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_swap",
     "aegkv_swap_blocks",
     "aegkv_copy_blocks",
+    "aegkv_copy_blocks_noalloc",
     "aegkv_migrate_blocks",
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
@@ -88,6 +89,7 @@ _SIGNATURES = {
          _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P],
     ),
     "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_copy_blocks_noalloc": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_transfer_entries": (
         _INT,

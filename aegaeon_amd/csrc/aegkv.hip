@@ -1165,11 +1165,16 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
 }
 
 // Whole-block copies from a source cache to a target cache (the same cache
-// for copy_blocks). Validates everything before touching the GPU.
-int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
-              const int64_t* page_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
-              int64_t num_pairs, const int64_t* src_ids, const int64_t* dst_ids, bool same_cache,
-              hipStream_t stream) {
+// for copy_blocks), in steps shared by the allocating and the
+// allocation-free entry points: layout checks, id checks, device-range
+// checks, the launch shape, then descriptor upload and launch.
+
+// Checks that need no HIP call and no memory: segment geometry and the
+// 16 B path. *max_page receives the largest page.
+int copy_check_layout(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
+                      const int64_t* page_bytes, int64_t src_num_blocks,
+                      int64_t dst_num_blocks, int64_t num_pairs, const int64_t* src_ids,
+                      const int64_t* dst_ids, bool same_cache, bool* vec, int64_t* max_page) {
   if (num_segments <= 0) return fail(AEGKV_EINVAL, "num_segments must be positive");
   if (!src_bases || !dst_bases || !page_bytes)
     return fail(AEGKV_EINVAL, "segment arrays must not be null");
@@ -1178,8 +1183,8 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   if (num_pairs < 0) return fail(AEGKV_EINVAL, "num_pairs must be >= 0");
   if (num_pairs > 0 && (!src_ids || !dst_ids))
     return fail(AEGKV_EINVAL, "block id arrays must not be null");
-  bool vec = true;
-  int64_t max_page = 0;
+  bool v = true;
+  int64_t mp = 0;
   for (int32_t s = 0; s < num_segments; ++s) {
     if (!src_bases[s] || !dst_bases[s]) return fail(AEGKV_EINVAL, "segment %d base is null", s);
     if (page_bytes[s] <= 0)
@@ -1198,11 +1203,17 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
                     "segment %d: source and target caches overlap (copy within one cache "
                     "with aegkv_copy_blocks)", s);
     }
-    vec = vec && aligned16(src_bases[s]) && aligned16(dst_bases[s]) && page_bytes[s] % 16 == 0;
-    max_page = std::max(max_page, page_bytes[s]);
+    v = v && aligned16(src_bases[s]) && aligned16(dst_bases[s]) && page_bytes[s] % 16 == 0;
+    mp = std::max(mp, page_bytes[s]);
   }
-  // target roles: 0 = untouched, 1 = source, 2 = target (sources only matter in one cache)
-  std::vector<uint8_t> role(static_cast<size_t>(dst_num_blocks), 0);
+  *vec = v;
+  *max_page = mp;
+  return 0;
+}
+
+// Every id inside its cache (first offending pair in pair order).
+int copy_check_ranges(int64_t src_num_blocks, int64_t dst_num_blocks, int64_t num_pairs,
+                      const int64_t* src_ids, const int64_t* dst_ids) {
   for (int64_t i = 0; i < num_pairs; ++i) {
     const int64_t s = src_ids[i], d = dst_ids[i];
     if (s < 0 || s >= src_num_blocks || d < 0 || d >= dst_num_blocks)
@@ -1210,23 +1221,57 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
                   static_cast<long long>(i), static_cast<long long>(s),
                   static_cast<long long>(d), static_cast<long long>(src_num_blocks),
                   static_cast<long long>(dst_num_blocks));
-    if (role[static_cast<size_t>(d)] == 2)
-      return fail(AEGKV_EDUP, "target block id %lld appears twice", static_cast<long long>(d));
-    if (role[static_cast<size_t>(d)] == 1)
-      return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
-                  static_cast<long long>(d));
-    role[static_cast<size_t>(d)] = 2;
   }
-  if (same_cache) {
-    for (int64_t i = 0; i < num_pairs; ++i) {
-      const int64_t s = src_ids[i];
-      if (role[static_cast<size_t>(s)] == 2)
-        return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
-                    static_cast<long long>(s));
-      role[static_cast<size_t>(s)] = 1;
-    }
+  return 0;
+}
+
+int dup_target(int64_t id) {
+  return fail(AEGKV_EDUP, "target block id %lld appears twice", static_cast<long long>(id));
+}
+
+int source_is_target(int64_t id) {
+  return fail(AEGKV_EOVERLAP, "block %lld is both a source and a target",
+              static_cast<long long>(id));
+}
+
+// Distinct targets, and (within one cache) no source that is also a
+// target, with a block-indexed map. Ids are in range.
+int copy_check_ids_map(int64_t dst_num_blocks, int64_t num_pairs, const int64_t* src_ids,
+                       const int64_t* dst_ids, bool same_cache) {
+  std::vector<uint8_t> target(static_cast<size_t>(dst_num_blocks), 0);
+  for (int64_t i = 0; i < num_pairs; ++i) {
+    uint8_t& t = target[static_cast<size_t>(dst_ids[i])];
+    if (t) return dup_target(dst_ids[i]);
+    t = 1;
   }
-  if (num_pairs == 0) return 0;
+  if (same_cache)
+    for (int64_t i = 0; i < num_pairs; ++i)
+      if (target[static_cast<size_t>(src_ids[i])]) return source_is_target(src_ids[i]);
+  return 0;
+}
+
+// The same checks without memory of the block count's size: sorted copies
+// of the ids in the caller's work arrays (num_pairs entries each).
+int copy_check_ids_sorted(int64_t num_pairs, const int64_t* src_ids, const int64_t* dst_ids,
+                          bool same_cache, int64_t* work_src, int64_t* work_dst) {
+  std::copy(dst_ids, dst_ids + num_pairs, work_dst);
+  std::sort(work_dst, work_dst + num_pairs);
+  for (int64_t i = 1; i < num_pairs; ++i)
+    if (work_dst[i] == work_dst[i - 1]) return dup_target(work_dst[i]);
+  if (!same_cache) return 0;
+  std::copy(src_ids, src_ids + num_pairs, work_src);
+  std::sort(work_src, work_src + num_pairs);
+  for (int64_t i = 0, j = 0; i < num_pairs && j < num_pairs;) {
+    if (work_src[i] == work_dst[j]) return source_is_target(work_src[i]);
+    if (work_src[i] < work_dst[j]) ++i;
+    else ++j;
+  }
+  return 0;
+}
+
+int copy_check_device(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
+                      const int64_t* page_bytes, int64_t src_num_blocks,
+                      int64_t dst_num_blocks, bool same_cache) {
   for (int32_t s = 0; s < num_segments; ++s) {
     int rc = check_device_range(src_bases[s], src_num_blocks * page_bytes[s], "segment base");
     if (rc) return rc;
@@ -1235,7 +1280,18 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
       if (rc) return rc;
     }
   }
-  const Tunables t = tunables();
+  return 0;
+}
+
+struct CopyPlan {
+  ShapeSel sh;
+  bool vec;
+  int64_t cpt;    // chunks per tile
+  int64_t items;  // work items (pair x segment x chunk)
+};
+
+int copy_plan(const Tunables& t, bool vec, int64_t max_page, int32_t num_segments,
+              int64_t num_pairs, CopyPlan* out) {
   ShapeSel sh = auto_shape(max_page);
   if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};
   if (!vec) sh = ShapeSel{256, 1};
@@ -1244,34 +1300,73 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   if (items >= (int64_t(1) << 32))
     return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
                 static_cast<long long>(items));
-  DeviceCtx* ctx = nullptr;
-  int rc = get_ctx(&ctx);
-  if (rc) return rc;
-  std::lock_guard<std::mutex> lk(ctx->mu);
-  const size_t seg_bytes = sizeof(CopySeg) * num_segments;
-  const size_t pair_off = (seg_bytes + 255) & ~size_t(255);
-  const size_t total = pair_off + sizeof(PairDesc) * num_pairs;
-  size_t off = 0;
-  rc = ring_reserve(ctx->ring, total, &off);
-  if (rc) return rc;
-  char* h = ctx->ring.host + off;
+  *out = CopyPlan{sh, vec, cpt, items};
+  return 0;
+}
+
+// Byte offset of the pair table after num_segments CopySeg entries.
+size_t copy_pair_offset(int32_t num_segments) {
+  return (sizeof(CopySeg) * static_cast<size_t>(num_segments) + 255) & ~size_t(255);
+}
+
+void pack_copy_desc(char* h, int32_t num_segments, void* const* src_bases,
+                    void* const* dst_bases, const int64_t* page_bytes, int64_t num_pairs,
+                    const int64_t* src_ids, const int64_t* dst_ids) {
   CopySeg* hs = reinterpret_cast<CopySeg*>(h);
   for (int32_t s = 0; s < num_segments; ++s)
     hs[s] = CopySeg{static_cast<const char*>(src_bases[s]), static_cast<char*>(dst_bases[s]),
                     page_bytes[s], 0};
-  PairDesc* hp = reinterpret_cast<PairDesc*>(h + pair_off);
+  PairDesc* hp = reinterpret_cast<PairDesc*>(h + copy_pair_offset(num_segments));
   for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_ids[i], dst_ids[i]};
+}
+
+// Launch the copy kernel over descriptors already on the device at `dv`.
+hipError_t copy_launch(const CopyPlan& p, const Tunables& t, int num_cus, int32_t num_segments,
+                       const char* dv, hipStream_t stream) {
+  return launch_copy(p.sh, p.vec, t.nt_stores != 0,
+                     launch_grid(t.copy_wgs_per_cu * num_cus, p.items, p.sh.wg),
+                     p.sh.wg == 1024 && p.sh.chunk() >= (int64_t(32) << 10)
+                         ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
+                     stream, reinterpret_cast<const CopySeg*>(dv),
+                     reinterpret_cast<const PairDesc*>(dv + copy_pair_offset(num_segments)),
+                     static_cast<uint32_t>(num_segments), static_cast<uint32_t>(p.items),
+                     static_cast<uint32_t>(p.cpt));
+}
+
+int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
+              const int64_t* page_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
+              int64_t num_pairs, const int64_t* src_ids, const int64_t* dst_ids, bool same_cache,
+              hipStream_t stream) {
+  bool vec = false;
+  int64_t max_page = 0;
+  int rc = copy_check_layout(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
+                             dst_num_blocks, num_pairs, src_ids, dst_ids, same_cache, &vec,
+                             &max_page);
+  if (!rc) rc = copy_check_ranges(src_num_blocks, dst_num_blocks, num_pairs, src_ids, dst_ids);
+  if (!rc) rc = copy_check_ids_map(dst_num_blocks, num_pairs, src_ids, dst_ids, same_cache);
+  if (rc || num_pairs == 0) return rc;
+  rc = copy_check_device(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
+                         dst_num_blocks, same_cache);
+  if (rc) return rc;
+  const Tunables t = tunables();
+  CopyPlan plan;
+  rc = copy_plan(t, vec, max_page, num_segments, num_pairs, &plan);
+  if (rc) return rc;
+  DeviceCtx* ctx = nullptr;
+  rc = get_ctx(&ctx);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const size_t total = copy_pair_offset(num_segments) + sizeof(PairDesc) * num_pairs;
+  size_t off = 0;
+  rc = ring_reserve(ctx->ring, total, &off);
+  if (rc) return rc;
+  char* h = ctx->ring.host + off;
+  pack_copy_desc(h, num_segments, src_bases, dst_bases, page_bytes, num_pairs, src_ids,
+                 dst_ids);
   char* dv = ctx->ring.dev + off;
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
-  e = launch_copy(sh, vec, t.nt_stores != 0,
-                  launch_grid(t.copy_wgs_per_cu * ctx->num_cus, items, sh.wg),
-                  sh.wg == 1024 && sh.chunk() >= (int64_t(32) << 10)
-                      ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
-                  stream, reinterpret_cast<const CopySeg*>(dv),
-                  reinterpret_cast<const PairDesc*>(dv + pair_off),
-                  static_cast<uint32_t>(num_segments), static_cast<uint32_t>(items),
-                  static_cast<uint32_t>(cpt));
+  e = copy_launch(plan, t, ctx->num_cus, num_segments, dv, stream);
   if (e != hipSuccess) {
     // the descriptor upload is already enqueued: retire its region in order
     (void)hipGetLastError();
@@ -1279,6 +1374,93 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
     return hip_fail(e, "copy_blocks_kernel launch");
   }
   return ring_commit(ctx->ring, off, total, stream);
+}
+
+// ------------------------------------------------ allocation-free copies --
+//
+// aegkv_copy_blocks_noalloc: aegkv_copy_blocks for callers that cannot
+// allocate. The descriptor (segment table + pair table) goes to `scratch`,
+// a fixed device array every GPU holds for the life of the process, instead
+// of the library's upload ring; the ids are checked with fixed host arrays
+// instead of a block-indexed map. Nothing is allocated on the host or the
+// device. Every call on a device shares that device's array, so calls that
+// overlap on one device (different streams, or threads) race; calls on one
+// stream are ordered.
+
+constexpr int32_t kNoAllocMaxSegments = 1024;
+constexpr int64_t kNoAllocMaxPairs = 65536;
+constexpr size_t kNoAllocBytes =
+    sizeof(CopySeg) * kNoAllocMaxSegments + sizeof(PairDesc) * kNoAllocMaxPairs;  // 1.03 MiB
+constexpr int kNoAllocMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+std::mutex g_noalloc_mu;                        // guards everything below
+char* g_scratch_ptr[kNoAllocMaxDevices] = {};   // device address of `scratch`, per device
+int g_noalloc_cus[kNoAllocMaxDevices] = {};
+alignas(256) unsigned char g_noalloc_host[kNoAllocBytes];  // descriptor packing (pageable)
+int64_t g_noalloc_work[2][kNoAllocMaxPairs];    // sorted id copies for the checks
+
+// Device address of this device's `scratch` (caller holds g_noalloc_mu).
+// hipGetSymbolAddress runs once per device, with that device current.
+int noalloc_scratch(int dev, char** out, int* num_cus) {
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return fail(AEGKV_EINVAL, "device %d is outside the %d devices the allocation-free "
+                "copy supports", dev, kNoAllocMaxDevices);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    AEGKV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    int cus = 0;
+    AEGKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    g_noalloc_cus[dev] = cus > 0 ? cus : 1;
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  *num_cus = g_noalloc_cus[dev];
+  return 0;
+}
+
+int copy_noalloc(int32_t num_segments, void* const* bases, const int64_t* page_bytes,
+                 int64_t num_blocks, int64_t num_pairs, const int64_t* src_ids,
+                 const int64_t* dst_ids, hipStream_t stream) {
+  if (num_segments > kNoAllocMaxSegments)
+    return fail(AEGKV_ENOMEM, "%d segments exceed the allocation-free copy's maximum of %d "
+                "(use aegkv_copy_blocks)", num_segments, kNoAllocMaxSegments);
+  if (num_pairs > kNoAllocMaxPairs)
+    return fail(AEGKV_ENOMEM, "%lld pairs exceed the allocation-free copy's maximum of %lld "
+                "(use aegkv_copy_blocks)", static_cast<long long>(num_pairs),
+                static_cast<long long>(kNoAllocMaxPairs));
+  bool vec = false;
+  int64_t max_page = 0;
+  int rc = copy_check_layout(num_segments, bases, bases, page_bytes, num_blocks, num_blocks,
+                             num_pairs, src_ids, dst_ids, true, &vec, &max_page);
+  if (!rc) rc = copy_check_ranges(num_blocks, num_blocks, num_pairs, src_ids, dst_ids);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  rc = copy_check_ids_sorted(num_pairs, src_ids, dst_ids, true, g_noalloc_work[0],
+                             g_noalloc_work[1]);
+  if (rc || num_pairs == 0) return rc;
+  rc = copy_check_device(num_segments, bases, bases, page_bytes, num_blocks, num_blocks, true);
+  if (rc) return rc;
+  const Tunables t = tunables();
+  CopyPlan plan;
+  rc = copy_plan(t, vec, max_page, num_segments, num_pairs, &plan);
+  if (rc) return rc;
+  int dev = -1;
+  AEGKV_HIP(hipGetDevice(&dev));
+  char* dv = nullptr;
+  int num_cus = 0;
+  rc = noalloc_scratch(dev, &dv, &num_cus);
+  if (rc) return rc;
+  pack_copy_desc(reinterpret_cast<char*>(g_noalloc_host), num_segments, bases, bases,
+                 page_bytes, num_pairs, src_ids, dst_ids);
+  const size_t total = copy_pair_offset(num_segments) + sizeof(PairDesc) * num_pairs;
+  // From pageable memory the runtime has taken the bytes when the call
+  // returns, so the packing area is free for the next call.
+  AEGKV_HIP(hipMemcpyAsync(dv, g_noalloc_host, total, hipMemcpyHostToDevice, stream));
+  hipError_t e = copy_launch(plan, t, num_cus, num_segments, dv, stream);
+  if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
+  return 0;
 }
 
 }  // namespace
@@ -1396,6 +1578,16 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
   return copy_core(num_segments, segment_bases, segment_bases, segment_page_bytes,
                    device_num_blocks, device_num_blocks, num_pairs, src_block_ids,
                    dst_block_ids, true, stream);
+}
+
+int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
+                              const int64_t* segment_page_bytes, int64_t device_num_blocks,
+                              int64_t num_pairs, const int64_t* src_block_ids,
+                              const int64_t* dst_block_ids, hipStream_t stream) {
+  g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
+  return copy_noalloc(num_segments, segment_bases, segment_page_bytes, device_num_blocks,
+                      num_pairs, src_block_ids, dst_block_ids, stream);
 }
 
 int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,

@@ -261,22 +261,10 @@ def swap_segments(
                                          mode=mode, stream=stream)
 
 
-def copy_blocks(
-    segments: Sequence[torch.Tensor],
-    src_block_ids,
-    dst_block_ids,
-    *,
-    segment_page_bytes: Sequence[int] | None = None,
-    device_num_blocks: int | None = None,
-    stream: torch.cuda.Stream | None = None,
-) -> None:
-    """In-HBM block copy: seg[dst[i]] := seg[src[i]] for every segment.
-
-    Each segment is viewed as [num_blocks, page] bytes; by default the page
-    is the tensor's bytes / size(0). Targets must be distinct and disjoint
-    from the sources. The reference has no KV copy_blocks; its in-HBM
-    compaction is aegaeon/allocator.py:101-137.
-    """
+def _copy_call_args(segments, src_block_ids, dst_block_ids, segment_page_bytes,
+                    device_num_blocks, stream):
+    """Checked C-ABI arguments of one copy_blocks call (device first; the
+    arrays are returned too so they outlive the call)."""
     if not segments:
         raise ValueError("at least one segment is required")
     dev = segments[0].device
@@ -299,13 +287,57 @@ def copy_blocks(
     if src.shape != dst.shape:
         raise ValueError("src and dst id lists differ in length")
     bases = (ctypes.c_void_p * len(segments))(*[t.data_ptr() for t in segments])
+    args = (len(segments), bases, _p64(page), int(device_num_blocks), src.size, _p64(src),
+            _p64(dst), _stream_ptr(dev, stream))
+    return dev, args, (page, src, dst)
+
+
+def copy_blocks(
+    segments: Sequence[torch.Tensor],
+    src_block_ids,
+    dst_block_ids,
+    *,
+    segment_page_bytes: Sequence[int] | None = None,
+    device_num_blocks: int | None = None,
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """In-HBM block copy: seg[dst[i]] := seg[src[i]] for every segment.
+
+    Each segment is viewed as [num_blocks, page] bytes; by default the page
+    is the tensor's bytes / size(0). Targets must be distinct and disjoint
+    from the sources. The reference has no KV copy_blocks; its in-HBM
+    compaction is aegaeon/allocator.py:101-137.
+    """
+    dev, args, _keep = _copy_call_args(segments, src_block_ids, dst_block_ids,
+                                       segment_page_bytes, device_num_blocks, stream)
     lib = _lib.load()
-    with torch.cuda.device(dev):
-        rc = lib.aegkv_copy_blocks(
-            len(segments), bases, _p64(page), int(device_num_blocks), src.size, _p64(src),
-            _p64(dst), _stream_ptr(dev, stream),
-        )
-    _lib.check(rc)
+    _lib.check(_call_on(dev, lambda: lib.aegkv_copy_blocks(*args)))
+
+
+#: limits of copy_blocks_noalloc (the fixed descriptor array of libaegkv)
+NOALLOC_MAX_SEGMENTS = 1024
+NOALLOC_MAX_PAIRS = 65536
+
+
+def copy_blocks_noalloc(
+    segments: Sequence[torch.Tensor],
+    src_block_ids,
+    dst_block_ids,
+    *,
+    segment_page_bytes: Sequence[int] | None = None,
+    device_num_blocks: int | None = None,
+    stream: torch.cuda.Stream | None = None,
+) -> None:
+    """copy_blocks through aegkv_copy_blocks_noalloc: the library allocates
+    nothing for the call (its descriptor goes to a fixed device array), for
+    callers that cannot allocate. At most NOALLOC_MAX_SEGMENTS segments and
+    NOALLOC_MAX_PAIRS pairs (ValueError beyond). Calls that overlap on one
+    device from different streams or threads race on that array; calls on
+    one stream are ordered."""
+    dev, args, _keep = _copy_call_args(segments, src_block_ids, dst_block_ids,
+                                       segment_page_bytes, device_num_blocks, stream)
+    lib = _lib.load()
+    _lib.check(_call_on(dev, lambda: lib.aegkv_copy_blocks_noalloc(*args)))
 
 
 def migrate_blocks(
@@ -539,3 +571,4 @@ def fence_wait(words: torch.Tensor, index: int, value: int, timed_out: torch.Ten
     rc = _call_on(dev, lambda: lib.aegkv_fence_wait(ptr, int(value), timeout_us, flag,
                                                     _stream_ptr(dev, stream)))
     _lib.check(rc)
+

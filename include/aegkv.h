@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define AEGKV_ABI_VERSION 1
+#define AEGKV_ABI_VERSION 2
 
 /* status codes (negative: rejected before any work was enqueued) */
 #define AEGKV_OK 0
@@ -45,7 +45,8 @@ extern "C" {
 #define AEGKV_EEXTENT (-4)       /* kernel-block extent outside the page     */
 #define AEGKV_EOVERLAP (-5)      /* copy: a source is also a target, or the
                                     migration's two caches overlap          */
-#define AEGKV_ENOMEM (-6)        /* output arrays too small for the rows     */
+#define AEGKV_ENOMEM (-6)        /* output arrays too small for the rows, or
+                                    a call beyond a fixed buffer's limit    */
 
 /* host-transfer designs for swap-out / swap-in */
 #define AEGKV_MODE_AUTO 0   /* library choice per direction: DIRECT unless
@@ -178,6 +179,25 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
                       int64_t device_num_blocks, int64_t num_pairs,
                       const int64_t* src_block_ids,
                       const int64_t* dst_block_ids, hipStream_t stream);
+
+/*
+ * aegkv_copy_blocks without allocating: same arguments, same checks, same
+ * kernels and the same result. No counterpart in the reference; it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The call allocates nothing on
+ * the host or the device: the descriptor goes to a fixed device array of
+ * 1,081,344 bytes that each GPU the library runs on holds until the process
+ * ends, and is copied there with hipMemcpyAsync from a fixed (pageable) host
+ * array, which the runtime has read when the call returns. Limits: at most
+ * 1024 segments and 65536 pairs per call (AEGKV_ENOMEM beyond, nothing
+ * enqueued). Every call on a device shares that device's array: calls that
+ * overlap on one device (from other streams or threads) race and must be
+ * ordered by the caller; calls on one stream are ordered by the stream.
+ */
+int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
+                              const int64_t* segment_page_bytes, int64_t device_num_blocks,
+                              int64_t num_pairs, const int64_t* src_block_ids,
+                              const int64_t* dst_block_ids, hipStream_t stream);
 
 /*
  * Block migration between two caches of the same layout: for every segment

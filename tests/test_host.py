@@ -448,23 +448,97 @@ def test_swap_blocks_rejections_before_any_hip_call(aegkv_lib, kwargs, code, wor
     assert word.encode() in aegkv_lib.aegkv_last_error()
 
 
-def test_copy_blocks_rejections_before_any_hip_call(aegkv_lib):
+@pytest.mark.parametrize("entry", ["aegkv_copy_blocks", "aegkv_copy_blocks_noalloc"])
+def test_copy_blocks_rejections_before_any_hip_call(aegkv_lib, entry):
     import numpy as np
 
     P64 = ctypes.POINTER(ctypes.c_int64)
     bases = (ctypes.c_void_p * 1)(0x10000)
     page = np.array([4096], np.int64)
+    fn = getattr(aegkv_lib, entry)
 
     def call(src, dst, blocks=8):
         s, d = np.array(src, np.int64), np.array(dst, np.int64)
-        return aegkv_lib.aegkv_copy_blocks(1, bases, page.ctypes.data_as(P64), blocks, s.size,
-                                           s.ctypes.data_as(P64), d.ctypes.data_as(P64), None)
+        return fn(1, bases, page.ctypes.data_as(P64), blocks, s.size, s.ctypes.data_as(P64),
+                  d.ctypes.data_as(P64), None)
 
     assert call([1, 2], [2, 3]) == -5
     assert call([1, 2], [3, 3]) == -3
     assert call([1], [8]) == -2
     assert call([1], [2], blocks=1 << 62) == -2
     assert call([], []) == 0  # nothing to do, nothing touched
+
+
+def _expected_copy_status(src, dst, blocks):
+    """Status the copy checks give: ranges (pair order), then duplicate
+    targets, then sources that are targets (brute force over the lists)."""
+    for s_, d_ in zip(src, dst):
+        if not (0 <= s_ < blocks and 0 <= d_ < blocks):
+            return -2
+    if len(set(dst)) != len(dst):
+        return -3
+    if set(src) & set(dst):
+        return -5
+    return 0
+
+
+def test_copy_blocks_noalloc_checks_agree_with_copy_blocks(aegkv_lib):
+    """The allocation-free entry checks ids by sorting where aegkv_copy_blocks
+    uses a block map: on random invalid lists both give the status the
+    brute-force rule gives (valid lists would reach the device checks)."""
+    import numpy as np
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+    bases = (ctypes.c_void_p * 1)(0x10000)
+    page = np.array([4096], np.int64)
+    rng = np.random.default_rng(77)
+    seen = set()
+    for _ in range(600):
+        blocks = int(rng.integers(2, 40))
+        n = int(rng.integers(1, 30))
+        src = rng.integers(-1, blocks + 1, n).astype(np.int64)
+        dst = rng.integers(-1, blocks + 1, n).astype(np.int64)
+        if rng.random() < 0.5:   # mostly in range, to reach the id checks
+            src, dst = np.clip(src, 0, blocks - 1), np.clip(dst, 0, blocks - 1)
+        want = _expected_copy_status(src.tolist(), dst.tolist(), blocks)
+        if want == 0:
+            continue
+        seen.add(want)
+        for entry in ("aegkv_copy_blocks", "aegkv_copy_blocks_noalloc"):
+            rc = getattr(aegkv_lib, entry)(1, bases, page.ctypes.data_as(P64), blocks, n,
+                                           src.ctypes.data_as(P64), dst.ctypes.data_as(P64),
+                                           None)
+            assert rc == want, (entry, src.tolist(), dst.tolist(), blocks)
+    assert seen == {-2, -3, -5}
+
+
+def test_copy_blocks_noalloc_limits(aegkv_lib):
+    """Calls beyond the fixed descriptor array are refused with a clear
+    error before anything else happens."""
+    import numpy as np
+
+    from aegaeon_amd import _lib, ops
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+    n = ops.NOALLOC_MAX_PAIRS + 1
+    ids = np.arange(n, dtype=np.int64)
+    page = np.full(ops.NOALLOC_MAX_SEGMENTS + 1, 4096, np.int64)
+    bases = (ctypes.c_void_p * page.size)(*([0x10000] * page.size))
+    fn = aegkv_lib.aegkv_copy_blocks_noalloc
+    rc = fn(1, bases, page.ctypes.data_as(P64), 2 * n, n, ids.ctypes.data_as(P64),
+            (ids + n).ctypes.data_as(P64), None)
+    assert rc == _lib.ENOMEM
+    assert b"65537 pairs exceed" in aegkv_lib.aegkv_last_error()
+    rc = fn(page.size, bases, page.ctypes.data_as(P64), 8, 1, ids.ctypes.data_as(P64),
+            (ids + 1).ctypes.data_as(P64), None)
+    assert rc == _lib.ENOMEM
+    assert b"1025 segments exceed" in aegkv_lib.aegkv_last_error()
+    # at the limits the size checks pass and the id checks run
+    m = ops.NOALLOC_MAX_PAIRS
+    dup = np.zeros(m, np.int64)
+    rc = fn(ops.NOALLOC_MAX_SEGMENTS, bases, page.ctypes.data_as(P64), 2 * m, m,
+            (ids[:m] + m).ctypes.data_as(P64), dup.ctypes.data_as(P64), None)
+    assert rc == _lib.EDUP
 
 
 def _run_with_env(env_extra, code):
