@@ -64,6 +64,8 @@ EXPORTED_SYMBOLS = (
     "aegkv_host_free",
     "aegkv_fence_signal",
     "aegkv_fence_wait",
+    "aegkv_fence_publish",
+    "aegkv_fence_host_wait",
     "aegkv_stream_create",
     "aegkv_stream_create_masked",
     "aegkv_stream_destroy",
@@ -101,6 +103,8 @@ _SIGNATURES = {
     "aegkv_host_free": (_INT, [_P]),
     "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
     "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),
+    "aegkv_fence_publish": (_INT, [_P, ctypes.c_uint64, _P]),
+    "aegkv_fence_host_wait": (_INT, [_P, ctypes.c_uint64, _I64]),
     "aegkv_stream_create": (_INT, [_PP]),
     "aegkv_stream_create_masked": (_INT, [_PP, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]),
     "aegkv_stream_destroy": (_INT, [_P]),

@@ -22,14 +22,23 @@
 //     flag word to 1, so no wave ever spins forever.
 //
 // Every memory operation here is a vector-memory load, store or atomic.
+//
+// A host-side view of the same counts serves a controller that only polls
+// completion on the CPU (the reference's BlockManager rebuilds the workers'
+// events and polls cudaEventQuery before it frees source blocks,
+// aegaeon/block_manager.py:804-851): aegkv_fence_publish enqueues a host
+// function that raises a host word, which may live in a file mapping shared
+// by every process, and aegkv_fence_host_wait reads it with a bounded wait.
 
 #include <hip/hip_runtime.h>
 #include "aegkv.h"
 #include "errors.h"
 
+#include <chrono>
 #include <cstdint>
 #include <mutex>
 #include <map>
+#include <thread>
 
 namespace {
 
@@ -106,9 +115,70 @@ int wall_clock_khz(int64_t* out) {
   return 0;
 }
 
+// Raise *word to at least value (release), from any host thread.
+void host_word_max(uint64_t* word, uint64_t value) {
+  uint64_t seen = __atomic_load_n(word, __ATOMIC_RELAXED);
+  while (seen < value &&
+         !__atomic_compare_exchange_n(word, &seen, value, true, __ATOMIC_RELEASE,
+                                      __ATOMIC_RELAXED)) {
+  }
+}
+
+struct Publish {
+  uint64_t* word;
+  uint64_t value;
+};
+
+// Runs on the runtime's host-function thread once the stream reaches it.
+void publish_cb(void* data) {
+  Publish* p = static_cast<Publish*>(data);
+  host_word_max(p->word, p->value);
+  delete p;
+}
+
+int check_host_word(const void* p) {
+  if (!p) return fail(AEGKV_EINVAL, "host fence word is null");
+  if (reinterpret_cast<uintptr_t>(p) & 7u)
+    return fail(AEGKV_EINVAL, "host fence word must be 8-byte aligned");
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
+
+int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream) {
+  aegkv_clear_error();
+  int rc = check_host_word(host_word);
+  if (rc) return rc;
+  if (value == 0 || value >= (uint64_t(1) << 63))
+    return fail(AEGKV_EINVAL, "fence values are positive and below 2^63");
+  Publish* p = new Publish{host_word, value};
+  hipError_t e = hipLaunchHostFunc(stream, publish_cb, p);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(e, "hipLaunchHostFunc(fence publish)");
+  }
+  return 0;
+}
+
+int aegkv_fence_host_wait(const uint64_t* host_word, uint64_t value, int64_t timeout_us) {
+  aegkv_clear_error();
+  int rc = check_host_word(host_word);
+  if (rc) return rc;
+  if (timeout_us < 0 || timeout_us > kMaxWaitMicros)
+    return fail(AEGKV_ERANGE, "host fence wait timeout %lld us outside [0, %lld]",
+                static_cast<long long>(timeout_us), static_cast<long long>(kMaxWaitMicros));
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(timeout_us);
+  for (int polls = 0;; ++polls) {
+    if (__atomic_load_n(host_word, __ATOMIC_ACQUIRE) >= value) return 1;
+    if (std::chrono::steady_clock::now() >= deadline) return 0;
+    // a few quick polls, then sleep in steps of at most 200 us
+    if (polls < 64) std::this_thread::yield();
+    else std::this_thread::sleep_for(std::chrono::microseconds(polls < 1000 ? 20 : 200));
+  }
+}
+
 
 int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream) {
   aegkv_clear_error();

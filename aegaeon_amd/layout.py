@@ -115,6 +115,26 @@ def allocate_composite_cache(tensor_specs: Sequence[KVCacheTensorSpec], num_bloc
     return CompositeCache(segments, raw, page, num_blocks, backing)
 
 
+def wrap_composite_cache(tensor_specs: Sequence[KVCacheTensorSpec], num_blocks: int,
+                         backing: Sequence[torch.Tensor]) -> CompositeCache:
+    """A CompositeCache over backing tensors that already exist, one per
+    spec in spec order: another process's cache opened through HIP IPC
+    memory handles (what the reference's worker exports for migration,
+    worker.py:2439-2445), or tensors allocated elsewhere. Sizes are checked;
+    nothing is copied or zeroed."""
+    if len(backing) != len(tensor_specs):
+        raise ValueError(f"{len(backing)} backing tensors for {len(tensor_specs)} specs")
+    segments, page = make_composite_layout(tensor_specs, num_blocks)
+    raw: Dict[str, torch.Tensor] = {}
+    for spec, t in zip(tensor_specs, backing):
+        if t.numel() * t.element_size() < spec.size:
+            raise ValueError(f"backing tensor of {t.numel() * t.element_size()} bytes is "
+                             f"smaller than its spec ({spec.size})")
+        for name in spec.shared_by:
+            raw[name] = t
+    return CompositeCache(segments, raw, page, num_blocks, list(backing))
+
+
 def host_page_geometry(composite_page_bytes: int, tp_size: int, element_size: int = 2
                        ) -> int:
     """Host bytes per block id: one composite page per TP rank

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import ctypes
 import sys
+import threading
 import weakref
 from typing import Sequence
 
@@ -572,3 +573,121 @@ def fence_wait(words: torch.Tensor, index: int, value: int, timed_out: torch.Ten
                                                     _stream_ptr(dev, stream)))
     _lib.check(rc)
 
+
+class HostFenceWords:
+    """Host fence words shared by processes: a file in /dev/shm of
+    `num_words` uint64 counters, mapped shared. Workers raise them behind
+    their swaps (fence_publish) and a controller in any process reads them
+    (fence_host_wait), where the reference's controller polls the workers'
+    interprocess events (aegaeon/block_manager.py:804-851).
+
+    HostFenceWords(n) creates a new zeroed file (its `name` is the path) and
+    removes it on close(); HostFenceWords.attach(name) maps an existing one.
+    """
+
+    def __init__(self, num_words: int | None = None, *, _name: str | None = None):
+        import mmap
+        import os
+        import uuid
+
+        if _name is None:
+            if num_words is None or num_words <= 0:
+                raise ValueError("num_words must be positive")
+            name = f"/dev/shm/aegkv-fence-{os.getpid()}-{uuid.uuid4().hex[:12]}"
+            fd = os.open(name, os.O_RDWR | os.O_CREAT | os.O_EXCL, 0o600)
+            try:
+                os.ftruncate(fd, 8 * int(num_words))
+            except BaseException:
+                os.close(fd)
+                os.unlink(name)
+                raise
+            self.owner = True
+        else:
+            name = _name
+            fd = os.open(name, os.O_RDWR)
+            self.owner = False
+        try:
+            size = os.fstat(fd).st_size
+            if size < 8 or size % 8:
+                raise ValueError(f"{name} is not a file of fence words ({size} bytes)")
+            self._mm = mmap.mmap(fd, size, mmap.MAP_SHARED, mmap.PROT_READ | mmap.PROT_WRITE)
+        finally:
+            os.close(fd)
+        self.name = name
+        self.num_words = size // 8
+        self._anchor = ctypes.c_char.from_buffer(self._mm)
+        self._base = ctypes.addressof(self._anchor)
+        self.words = np.frombuffer(self._mm, dtype=np.uint64)
+
+    @classmethod
+    def attach(cls, name: str) -> "HostFenceWords":
+        return cls(_name=name)
+
+    def ptr(self, index: int) -> int:
+        if self._mm is None:
+            raise ValueError("these host fence words are closed")
+        if not 0 <= index < self.num_words:
+            raise ValueError(f"host fence index {index} outside [0, {self.num_words})")
+        return self._base + 8 * index
+
+    def close(self) -> None:
+        """Unmap (and remove the file, for the creator). Callers first make
+        sure no stream still holds a publish into these words."""
+        import os
+
+        if self._mm is None:
+            return
+        self.words = None
+        self._anchor = None
+        self._mm.close()
+        self._mm = None
+        if self.owner:
+            try:
+                os.unlink(self.name)
+            except FileNotFoundError:
+                pass
+
+
+_attached_lock = threading.Lock()
+_attached: dict = {}
+
+
+def attached_host_fence_words(name: str) -> HostFenceWords:
+    """This process's mapping of the host fence words at `name` (mapped once,
+    kept until the process ends)."""
+    with _attached_lock:
+        hw = _attached.get(name)
+        if hw is None or hw._mm is None:
+            hw = HostFenceWords.attach(name)
+            _attached[name] = hw
+        return hw
+
+
+def fence_publish(host_words: HostFenceWords, index: int, value: int, *,
+                  device: torch.device | None = None,
+                  stream: torch.cuda.Stream | None = None) -> None:
+    """Raise host_words[index] to at least `value` once every operation
+    enqueued earlier on `stream` (default: the current stream of `device`)
+    has finished (aegkv_fence_publish, a host function on the stream)."""
+    if not 0 < value < (1 << 63):
+        raise ValueError("fence values are positive and below 2**63")
+    ptr = host_words.ptr(index)
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    lib = _lib.load()
+    rc = _call_on(dev, lambda: lib.aegkv_fence_publish(ptr, int(value), _stream_ptr(dev, stream)))
+    _lib.check(rc)
+
+
+def fence_host_wait(host_words: HostFenceWords, index: int, value: int,
+                    timeout_s: float = 0.0) -> bool:
+    """True once host_words[index] >= value; waits on this thread for at most
+    timeout_s seconds (0: look once). No GPU call; the GIL is released."""
+    if not 0 < value < (1 << 63):
+        raise ValueError("fence values are positive and below 2**63")
+    if timeout_s < 0:
+        raise ValueError("timeout_s must be >= 0")
+    rc = _lib.load().aegkv_fence_host_wait(host_words.ptr(index), int(value),
+                                           int(timeout_s * 1e6))
+    if rc < 0:
+        _lib.check(rc)
+    return rc == 1

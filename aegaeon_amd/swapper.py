@@ -19,7 +19,11 @@ which each swapper owns one word per swap stream (fence_slots). After each
 swap the swapper raises its word to the next count on that stream and
 publishes FenceToken(word, count) as last_fence; a swap in another process
 that lists the token among its source events waits on the device until the
-word has reached the count. Ray object refs are not part of this module.
+word has reached the count. With fence_host (host fence words in a shared
+/dev/shm file) the swapper also publishes each count to the host behind the
+swap, so a controller in any process can poll the token on the CPU
+(FenceToken.query / synchronize) before it frees the move's source blocks.
+Ray object refs are not part of this module.
 """
 
 from __future__ import annotations
@@ -42,11 +46,56 @@ logger = logging.getLogger("aegaeon_amd.swap")
 @dataclass(frozen=True)
 class FenceToken:
     """Completion of a swap as a fence: the swap has finished once
-    fence_words[slot] >= value. Plain ints, so it crosses process
-    boundaries like the reference's event handle bytes."""
+    fence_words[slot] >= value. Plain ints (and a file name), so it crosses
+    process boundaries like the reference's event handle bytes.
+
+    With `host` (the name of the swapper's HostFenceWords) the token also
+    answers on the CPU, in any process: query() and synchronize() read the
+    host word the swapper publishes behind the swap, which is how a
+    controller polls a worker's move before it frees the source blocks
+    (the reference polls the rebuilt IPC events, block_manager.py:804-851).
+    That makes a token a move event for BlockPools.record_move.
+    """
 
     slot: int
     value: int
+    host: Optional[str] = None
+
+    def _host_words(self) -> "ops.HostFenceWords":
+        if self.host is None:
+            raise ValueError("this FenceToken has no host fence words; give the swapper "
+                             "fence_host=HostFenceWords(...) to poll moves on the CPU")
+        return ops.attached_host_fence_words(self.host)
+
+    def query(self) -> bool:
+        """True once the swap behind this token has finished."""
+        return ops.fence_host_wait(self._host_words(), self.slot, self.value, 0.0)
+
+    def synchronize(self, timeout_s: float = 600.0) -> None:
+        """Block this thread until the swap has finished; TimeoutError after
+        timeout_s seconds."""
+        if not ops.fence_host_wait(self._host_words(), self.slot, self.value, timeout_s):
+            raise TimeoutError(f"fence {self.slot} did not reach {self.value} within "
+                               f"{timeout_s} s")
+
+
+_ipc_event_refusal: Dict[int, Optional[str]] = {}
+
+
+def interprocess_event_refusal(device: torch.device) -> Optional[str]:
+    """None if this process's HIP runtime records interprocess events on
+    `device`, else the error it gave (tried once per device)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _ipc_event_refusal:
+        try:
+            with torch.cuda.device(index):
+                ev = torch.cuda.Event(interprocess=True)
+                ev.record(torch.cuda.current_stream(index))
+                ev.synchronize()
+            _ipc_event_refusal[index] = None
+        except RuntimeError as exc:
+            _ipc_event_refusal[index] = str(exc).strip().splitlines()[0]
+    return _ipc_event_refusal[index]
 
 
 class KVSwapper:
@@ -58,7 +107,9 @@ class KVSwapper:
                  host_element_size: int = 2, interprocess_events: bool = False,
                  fence_words: Optional[torch.Tensor] = None,
                  fence_slots: Optional[Tuple[int, int]] = None,
-                 fence_timeout_s: float = 30.0, dedicated_streams: bool = False,
+                 fence_timeout_s: float = 30.0,
+                 fence_host: Optional[Union["ops.HostFenceWords", str]] = None,
+                 dedicated_streams: bool = False,
                  swap_cu_mask: Optional[Sequence[int]] = None, mode: str = "auto"):
         if len(group_layer_names) != len(group_descriptors):
             raise ValueError("one layer-name set per cache group is required")
@@ -118,6 +169,13 @@ class KVSwapper:
                 self._extents_per_entry[g] += 1
         device = self._segments[0].device
         self.device = device
+        if interprocess_events:
+            refusal = interprocess_event_refusal(device)
+            if refusal is not None:
+                raise ValueError(
+                    f"this HIP runtime refuses to record interprocess events ({refusal}); "
+                    "order moves across processes with fences instead (fence_words, "
+                    "fence_slots and, for CPU-side completion, fence_host)")
         self._layout = ops.SegmentLayout(
             self._segments, self._page, self._cpu_off, self._owner_mask, cache.num_blocks,
             self._kpp, self.kv_swap_view.view(-1), self.host_page_bytes,
@@ -155,6 +213,15 @@ class KVSwapper:
                         raise ValueError(f"fence slot {w} outside the fence words")
                 if fence_slots[0] == fence_slots[1]:
                     raise ValueError("each swap stream needs its own fence word")
+        if fence_host is not None:
+            if fence_slots is None:
+                raise ValueError("fence_host needs fence_slots")
+            if isinstance(fence_host, str):
+                fence_host = ops.attached_host_fence_words(fence_host)
+            for w in fence_slots:
+                if not 0 <= w < fence_host.num_words:
+                    raise ValueError(f"fence slot {w} outside the host fence words")
+        self.fence_host = fence_host
         self.fence_words = fence_words
         self.fence_slots = tuple(fence_slots) if fence_slots is not None else None
         self.fence_timeout_s = fence_timeout_s
@@ -244,9 +311,14 @@ class KVSwapper:
     def _signal(self, side: int, stream) -> None:
         if self.fence_slots is not None:
             self._fence_count[side] += 1
-            ops.fence_signal(self.fence_words, self.fence_slots[side], self._fence_count[side],
-                             stream=stream)
-            self.last_fence = FenceToken(self.fence_slots[side], self._fence_count[side])
+            slot, count = self.fence_slots[side], self._fence_count[side]
+            ops.fence_signal(self.fence_words, slot, count, stream=stream)
+            host = None
+            if self.fence_host is not None:
+                ops.fence_publish(self.fence_host, slot, count, device=self.device,
+                                  stream=stream)
+                host = self.fence_host.name
+            self.last_fence = FenceToken(slot, count, host)
 
     def register_peer_cache(self, engine_id: int, segment_pages: Sequence[torch.Tensor]) -> None:
         """Make another engine's cache a migration source

@@ -332,6 +332,30 @@ int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream);
 int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
                      uint64_t* timed_out, hipStream_t stream);
 
+/*
+ * Host-side fence completion, for a controller that polls moves on the CPU
+ * before it frees their source blocks. Replaces the controller half of the
+ * reference's event chaining: BlockManager._reclaim_blocks rebuilds the
+ * workers' interprocess events and polls cudaEventQuery
+ * (aegaeon/block_manager.py:804-851, handles from aegaeon/utils.py:263-288).
+ *
+ * A host fence word is an 8-byte aligned uint64 in host memory; to be read
+ * by other processes it lives in a mapping they share (a /dev/shm file).
+ *
+ * aegkv_fence_publish: once every operation enqueued on `stream` before it
+ * has finished, raise *host_word to at least `value` (0 < value < 2^63;
+ * atomic max, release). It is a host function on the stream (hipLaunchHostFunc):
+ * the stream is held by the runtime, no wave waits on a CU. The mapping must
+ * stay valid until the stream has passed it.
+ *
+ * aegkv_fence_host_wait: on the calling thread, wait until *host_word >=
+ * value (acquire), for at most timeout_us microseconds (0: look once;
+ * at most 600 s). Returns 1 once reached, 0 if not within the time, a
+ * negative status on a bad argument. No HIP call.
+ */
+int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream);
+int aegkv_fence_host_wait(const uint64_t* host_word, uint64_t value, int64_t timeout_us);
+
 #ifdef __cplusplus
 }
 #endif

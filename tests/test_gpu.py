@@ -1121,11 +1121,52 @@ def _ipc_producer(q_in, q_out):
     q_in.get()  # keep the event and tensor alive until the parent is done
 
 
-@pytest.mark.skip(reason="the HIP runtime here rejects recording interprocess events "
-                         "(torch.cuda.Event(interprocess=True).record -> hipErrorInvalidValue); "
-                         "cross-process ordering is covered by fences instead "
-                         "(test_swap_waits_on_fence_from_another_process)")
-def test_swap_waits_on_ipc_event_from_another_process(gpu):
+def _hip_interprocess_event_status():
+    """(create, export, record) statuses of an interprocess event, straight
+    from the HIP runtime torch loaded (hipEventInterprocess 0x4 |
+    hipEventDisableTiming 0x2), recorded on the null stream."""
+    hip = ctypes.CDLL("libamdhip64.so.7")   # the runtime already loaded by torch
+    ev = ctypes.c_void_p()
+    create = hip.hipEventCreateWithFlags(ctypes.byref(ev), ctypes.c_uint(0x6))
+    if create != 0:
+        return create, None, None
+    handle = (ctypes.c_char * 64)()
+    export = hip.hipIpcGetEventHandle(handle, ev)
+    record = hip.hipEventRecord(ev, ctypes.c_void_p(0))
+    hip.hipDeviceSynchronize()
+    hip.hipGetLastError()
+    hip.hipEventDestroy(ev)
+    return create, export, record
+
+
+def test_interprocess_event_contract(gpu):
+    """The reference chains moves across processes with interprocess events
+    (worker.py:2249,2331,2349 record and export; :2351-2394 open and wait).
+    This runtime creates them but refuses to export or record them
+    (hipErrorInvalidValue = 1): then a swapper asked for interprocess
+    events refuses up front, naming the fence path instead. If the runtime
+    exports and records them, the reference's handle path must work end to
+    end."""
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import KVSwapper
+
+    create, export, record = _hip_interprocess_event_status()
+    _say("interprocess event statuses (create, export, record):", create, export, record)
+    assert create == 0
+    if export != 0 or record != 0:
+        assert 1 in (export, record), (export, record)   # hipErrorInvalidValue
+        cache = allocate_composite_cache([KVCacheTensorSpec(16 * 4096, ("l0",))], 16, gpu)
+        pool = ops.PinnedHostPool(4 * 4096)
+        with pytest.raises(ValueError, match="fence"):
+            KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)],
+                      pool.tensor, interprocess_events=True)
+        pool.free()
+        return
+    _swap_waits_on_ipc_event_from_another_process(gpu)
+
+
+def _swap_waits_on_ipc_event_from_another_process(gpu):
     """A source event exported by another process orders the swap after that
     process's write (worker.py:2351-2394)."""
     import time
@@ -1467,6 +1508,134 @@ def test_swap_waits_on_fence_from_another_process(gpu):
         if child.is_alive():
             child.kill()
     pool.free()
+
+
+def test_fence_publish_follows_stream_work(gpu):
+    """A host fence word is raised only after the work enqueued before the
+    publish: here a device fence wait that the test releases from another
+    stream, so the host word stays low until then (no timing involved)."""
+    words = torch.zeros(2, dtype=torch.int64, device=gpu)
+    flags = torch.zeros(1, dtype=torch.int64, device=gpu)
+    hw = ops.HostFenceWords(2)
+    try:
+        a, b = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+        torch.cuda.synchronize()
+        ops.fence_wait(words, 0, 1, flags, timeout_s=60, stream=a)
+        ops.fence_publish(hw, 1, 9, device=gpu, stream=a)
+        assert not ops.fence_host_wait(hw, 1, 9, timeout_s=0.2)
+        ops.fence_signal(words, 0, 1, stream=b)
+        assert ops.fence_host_wait(hw, 1, 9, timeout_s=60)
+        a.synchronize()
+        assert int(flags[0]) == 0 and int(hw.words[1]) == 9
+        ops.fence_publish(hw, 1, 4, device=gpu, stream=a)   # a smaller count never lowers it
+        a.synchronize()
+        assert int(hw.words[1]) == 9
+    finally:
+        torch.cuda.synchronize()
+        hw.close()
+
+
+def _reclaim_worker(q_in, q_out):
+    """Child process (a worker): open the controller's cache, device fence
+    words and host fence words, swap the planned blocks out behind the
+    controller's "go" fence, hand back the swap's FenceToken without
+    waiting, and on request report whether the host pages hold the bytes
+    the source blocks had before the swap."""
+    import torch
+
+    from aegaeon_amd import ops as cops
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import kv_tensor_specs, wrap_composite_cache
+    from aegaeon_amd.swapper import FenceToken, KVSwapper
+
+    torch.cuda.set_device(0)
+    backing, words, host_name, geometry, lists = q_in.get()
+    n_layers, n_blocks, heads, dim, n_host = geometry
+    rids, src, dst, grp, first, valid = lists
+    cache = wrap_composite_cache(kv_tensor_specs(n_layers, n_blocks, 16, heads, dim, 2),
+                                 n_blocks, backing)
+    S = len(cache.segments)
+    pool = cops.PinnedHostPool(n_host * cache.page_size_bytes)
+    names = [{s.layer_name for s in cache.segments}]
+    sw = KVSwapper(cache, names, [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
+                   fence_words=words, fence_slots=(0, 1), fence_host=host_name,
+                   fence_timeout_s=60)
+    si = torch.tensor(src, device="cuda")
+    expect = [cache.segment_pages(i)[si].clone() for i in range(S)]
+    torch.cuda.synchronize()
+    sw.swap_blocks(rids, src, dst, grp, first, valid,
+                   [FenceToken(4, 1)] + [None] * (len(rids) - 1), False)
+    q_out.put(sw.last_fence)
+    assert q_in.get() == "check"
+    sw.wait_for_all_move_out()
+    pages = pool.tensor.view(n_host, S, -1)[torch.tensor(dst)].to("cuda")
+    q_out.put(all(torch.equal(pages[:, i], expect[i]) for i in range(S)))
+    q_in.get()   # keep the shared memory open until the controller is done
+    sw.close()
+
+
+def test_controller_reclaims_after_worker_fence_across_processes(gpu):
+    """The controller half of the reference's move chaining
+    (block_manager.py:804-851): a worker process swaps a plan's blocks out
+    and hands back a FenceToken; the controller's BlockPools keeps the
+    source ids until the token completes on the host, frees them then, and
+    at once overwrites the freed blocks. The worker's host pages must hold
+    the old bytes: the sources were freed only after the swap read them."""
+    from aegaeon_amd.cache_groups import BLOCK_LOCATION_CPU, BlockTable, CacheGroupConfig
+    from aegaeon_amd.layout import allocate_composite_cache, kv_tensor_specs
+    from aegaeon_amd.planner import BlockPools, plan_move
+
+    _say("controller reclaim after a worker's fence across processes")
+    n_layers, n_blocks, heads, dim = 8, 256, 16, 128       # 16 x 64 KiB tiles, 1 MiB pages
+    cache = allocate_composite_cache(kv_tensor_specs(n_layers, n_blocks, 16, heads, dim, 2),
+                                     n_blocks, gpu)
+    for t in cache.backing:
+        t.random_(-128, 127)
+    page = cache.page_size_bytes
+    n_host = 256
+    groups = (CacheGroupConfig("attention", 16, 16),)
+    shape = (page // 2,)
+    pools = BlockPools(cpu_num_slabs=1, cpu_slab_size_bytes=n_host * page)
+    pools.register_gpu_space(0, n_blocks, shape, groups)
+    tables = {r: BlockTable(0, shape, groups, [pools.allocate(60, 0, shape)]) for r in range(4)}
+    plan = plan_move([(r, 60 * 16) for r in range(4)], tables, BLOCK_LOCATION_CPU, pools)
+    free_before = list(pools.gpu_free_blocks[0])
+    words = torch.zeros(8, dtype=torch.int64, device=gpu)
+    hw = ops.HostFenceWords(8)
+    torch.cuda.synchronize()
+    mp = torch.multiprocessing.get_context("spawn")
+    q_in, q_out = mp.Queue(), mp.Queue()
+    child = mp.Process(target=_reclaim_worker, args=(q_in, q_out), daemon=True)
+    child.start()
+    try:
+        lists = (plan.request_ids, plan.source_block_ids, plan.target_block_ids, plan.group_ids,
+                 plan.first_kernel_blocks, plan.valid_kernel_blocks)
+        q_in.put((cache.backing, words, hw.name, (n_layers, n_blocks, heads, dim, n_host),
+                  lists))
+        token = q_out.get(timeout=200)
+        assert token.host == hw.name and token.slot == 0 and token.value == 1
+        pools.record_move(plan, [token])
+        assert pools.reclaim_gpu_moves(0, wait=False) == (0, 0)   # waiting for "go"
+        assert not token.query()
+        assert pools.gpu_free_blocks[0] == free_before
+        ops.fence_signal(words, 4, 1)                            # go
+        n = len(plan.release_source_block_ids)
+        assert pools.reclaim_gpu_moves(0, wait=True) == (1, n)
+        assert token.query()
+        freed = torch.tensor(plan.release_source_block_ids, device=gpu)
+        for i in range(len(cache.segments)):
+            cache.segment_pages(i).index_fill_(0, freed, 0x5A)   # reuse at once
+        torch.cuda.synchronize()
+        assert sorted(pools.gpu_free_blocks[0]) == sorted(free_before +
+                                                           plan.release_source_block_ids)
+        q_in.put("check")
+        assert q_out.get(timeout=100) is True, "the worker's swap read blocks after their reuse"
+    finally:
+        q_in.put(None)
+        child.join(60)
+        if child.is_alive():
+            child.kill()
+        hw.close()
 
 
 def test_tensor_parallel_ranks_share_host_pages(gpu):

@@ -364,6 +364,54 @@ def test_fence_rejections_before_any_hip_call(aegkv_lib):
         ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 0)
 
 
+def test_host_fence_words_across_processes(aegkv_lib):
+    """Host fence words live in a shared file: a value written by another
+    process is seen by fence_host_wait here, with a bounded wait; the
+    creator removes the file on close."""
+    import os
+    import sys
+    import time
+
+    from aegaeon_amd import ops
+
+    hw = ops.HostFenceWords(3)
+    assert hw.name.startswith("/dev/shm/") and hw.num_words == 3
+    assert not ops.fence_host_wait(hw, 1, 1)
+    code = ("import sys, time; sys.path.insert(0, '.'); from aegaeon_amd import ops; "
+            f"h = ops.HostFenceWords.attach({hw.name!r}); time.sleep(0.3); h.words[1] = 7; "
+            "h.close()")
+    proc = subprocess.Popen([sys.executable, "-c", code], cwd=str(REPO))
+    t0 = time.perf_counter()
+    assert ops.fence_host_wait(hw, 1, 7, timeout_s=60)
+    assert time.perf_counter() - t0 >= 0.2
+    assert proc.wait(60) == 0
+    assert ops.fence_host_wait(hw, 1, 6) and not ops.fence_host_wait(hw, 1, 8, 0.02)
+    with pytest.raises(ValueError):
+        hw.ptr(3)
+    name = hw.name
+    hw.close()
+    assert not os.path.exists(name)
+
+
+def test_host_fence_rejections_before_any_hip_call(aegkv_lib):
+    from aegaeon_amd import _lib
+
+    lib = aegkv_lib
+    word = (ctypes.c_uint64 * 2)()
+    base = ctypes.addressof(word)
+    assert lib.aegkv_fence_publish(None, 1, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base + 4, 1, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base, 0, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base, 1 << 63, None) == _lib.EINVAL
+    assert lib.aegkv_fence_host_wait(None, 1, 0) == _lib.EINVAL
+    assert lib.aegkv_fence_host_wait(base + 1, 1, 0) == _lib.EINVAL
+    assert lib.aegkv_fence_host_wait(base, 1, -1) == _lib.ERANGE
+    assert lib.aegkv_fence_host_wait(base, 1, 601_000_000) == _lib.ERANGE
+    word[0] = 5
+    assert lib.aegkv_fence_host_wait(base, 5, 0) == 1
+    assert lib.aegkv_fence_host_wait(base, 6, 1000) == 0
+
+
 def test_tuning_knobs(aegkv_lib):
     from aegaeon_amd import _lib
 

@@ -235,6 +235,42 @@ def test_move_ledger_reclaims_in_record_order():
     assert pools.reclaim_gpu_moves(0) == (0, 0)
 
 
+def test_move_ledger_takes_fence_tokens():
+    """A FenceToken with host fence words is a move event: the ledger frees
+    the sources once the host word reaches the token's count, and a
+    waiting reclaim returns once another thread publishes it (the
+    controller's poll of block_manager.py:804-851, with host words in place
+    of rebuilt IPC events)."""
+    import threading
+    import time
+
+    from aegaeon_amd import ops
+    from aegaeon_amd.swapper import FenceToken
+
+    hw = ops.HostFenceWords(4)
+    try:
+        pools, tables = _engine_with_requests(2, 4)
+        p0 = plan_move([(0, 64)], tables, BLOCK_LOCATION_CPU, pools)
+        p1 = plan_move([(1, 64)], tables, BLOCK_LOCATION_CPU, pools)
+        pools.record_move(p0, [FenceToken(2, 3, hw.name)])
+        pools.record_move(p1, [FenceToken(2, 4, hw.name), FenceToken(3, 1, hw.name)])
+        hw.words[2] = 2
+        assert pools.reclaim_gpu_moves(0, wait=False) == (0, 0)
+        hw.words[2] = 4
+        assert pools.reclaim_gpu_moves(0, wait=False) == (1, 4)   # p1 needs word 3 too
+        threading.Timer(0.2, lambda: hw.words.__setitem__(3, 1)).start()
+        t0 = time.perf_counter()
+        assert pools.reclaim_gpu_moves(0, wait=True) == (1, 4)
+        assert time.perf_counter() - t0 >= 0.15
+        assert sorted(pools.gpu_free_blocks[0]) == list(range(1, 12))
+        with pytest.raises(TimeoutError):
+            FenceToken(0, 1, hw.name).synchronize(timeout_s=0.05)
+        with pytest.raises(ValueError, match="no host fence words"):
+            FenceToken(0, 1).query()
+    finally:
+        hw.close()
+
+
 def test_gpu_allocation_waits_for_swap_outs():
     """A GPU allocation the free list cannot serve waits for the engine's
     swap-outs and takes back their sources (block_manager.py:956-970)."""
