@@ -46,7 +46,10 @@ TUNE_SWAP_UNROLL = 12
 TUNE_STAGED_WORKGROUPS = 13
 TUNE_STAGED_OVERLAP = 14
 TUNE_SWAP_OUT_WORKGROUPS_UNCACHED = 15
+TUNE_COPY_LANES = 17
 HOST_UNCACHED = 1
+PROBE_READ = 1
+PROBE_WRITE = 2
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (
@@ -57,6 +60,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_swap_blocks",
     "aegkv_copy_blocks",
     "aegkv_copy_blocks_noalloc",
+    "aegkv_copy_probe",
     "aegkv_migrate_blocks",
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
@@ -92,6 +96,8 @@ _SIGNATURES = {
     ),
     "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_copy_blocks_noalloc": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_copy_probe": (_INT, [_INT, _I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P,
+                                ctypes.c_uint32, _P]),
     "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_transfer_entries": (
         _INT,

@@ -94,6 +94,7 @@ struct Tunables {
   int64_t nt_stores = 1;
   int64_t copy_wgs_per_cu = 0;   // copy_blocks: 0 = one workgroup per work item
   int64_t copy_unroll = 0;       // copy_blocks: 0 = shape from the page size
+  int64_t copy_lanes = 0;        // copy_blocks with copy_unroll: 256 or 1024 lanes (0 = 1024)
   int64_t swap_shape_auto = 0;   // swap kernels: 1 = page-sized shape as copy_blocks
   int64_t swap_unroll = 2;       // swap kernels: 16 B loads per lane (256-lane shape)
   int64_t staged_workgroups = 0; // STAGED gather/scatter grid: 0 = one workgroup per item
@@ -308,6 +309,65 @@ __global__ __launch_bounds__(WG) void copy_blocks_kernel(
       move_chunk16<WG, U, NT_STORE>(src, dst, nbytes);
     else
       move_chunk_bytes<WG>(src, dst, nbytes);
+  }
+}
+
+// Measurement twins of copy_blocks_kernel (aegkv_copy_probe): the same
+// item walk over the same tiles and the same grid, either reading the
+// source tiles only (PROBE_READ; the loads are XOR-folded and the fold is
+// stored only if it equals `magic`, so no load can be dropped and nearly
+// nothing is written) or writing a fixed pattern to the target tiles only
+// (PROBE_WRITE). Their rates bound what a copy of that tile pattern can
+// reach on the memory system at hand.
+constexpr int PROBE_READ = 1;
+constexpr int PROBE_WRITE = 2;
+
+template <int WG, int U, int KIND, bool NT_STORE>
+__global__ __launch_bounds__(WG) void copy_probe_kernel(
+    const CopySeg* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
+    uint32_t num_items, uint32_t chunks_per_tile, uint32_t* sink, uint32_t magic) {
+  constexpr int64_t kChunk = Shape<WG, U>::kChunk;
+  const uint32_t tid = threadIdx.x;
+  v4u acc = {0u, 0u, 0u, 0u};
+  const v4u pattern = {tid, blockIdx.x, 0x5a5a5a5au, magic};
+  for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
+    const uint32_t tile = w / chunks_per_tile;
+    const uint32_t c = w - tile * chunks_per_tile;
+    const uint32_t p = tile / num_segs;
+    const uint32_t s = tile - p * num_segs;
+    const PairDesc pr = pairs[p];
+    const CopySeg seg = segs[s];
+    const int64_t begin = static_cast<int64_t>(c) * kChunk;
+    if (begin >= seg.page_bytes) continue;
+    const uint32_t n16 = static_cast<uint32_t>(
+        ((seg.page_bytes - begin < kChunk) ? (seg.page_bytes - begin) : kChunk) >> 4);
+    if (KIND == PROBE_READ) {
+      const gv4u* src = (const gv4u*)(seg.src + pr.src * seg.page_bytes + begin);
+      v4u r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t i = tid + u * WG;
+        r[u] = i < n16 ? __builtin_nontemporal_load(src + i) : v4u{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= r[u];
+    } else {
+      gv4u* dst = (gv4u*)(seg.dst + pr.dst * seg.page_bytes + begin);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t i = tid + u * WG;
+        if (i < n16) {
+          if (NT_STORE)
+            __builtin_nontemporal_store(pattern, dst + i);
+          else
+            dst[i] = pattern;
+        }
+      }
+    }
+  }
+  if (KIND == PROBE_READ) {
+    const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    if (x == magic) sink[0] = x;
   }
 }
 
@@ -623,10 +683,39 @@ hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, unsigned ld
   if (sh.wg == W && sh.u == UU)                                                       \
     return nt ? launch_copy_t<W, UU, true, true>(grid, lds, st, s, p, ns, items, cpt) \
               : launch_copy_t<W, UU, true, false>(grid, lds, st, s, p, ns, items, cpt);
-  AEGKV_CP(256, 1) AEGKV_CP(256, 2) AEGKV_CP(256, 4)
+  AEGKV_CP(256, 1) AEGKV_CP(256, 2) AEGKV_CP(256, 4) AEGKV_CP(256, 8)
   AEGKV_CP(1024, 1) AEGKV_CP(1024, 2) AEGKV_CP(1024, 3) AEGKV_CP(1024, 4)
   AEGKV_CP(1024, 5) AEGKV_CP(1024, 6) AEGKV_CP(1024, 8) AEGKV_CP(1024, 10)
 #undef AEGKV_CP
+  return hipErrorInvalidValue;
+}
+
+template <int WG, int U, int KIND, bool NT>
+hipError_t launch_probe_t(int64_t grid, unsigned lds, hipStream_t st, const CopySeg* s,
+                          const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt,
+                          uint32_t* sink, uint32_t magic) {
+  hipLaunchKernelGGL((copy_probe_kernel<WG, U, KIND, NT>), dim3(static_cast<uint32_t>(grid)),
+                     dim3(WG), lds, st, s, p, ns, items, cpt, sink, magic);
+  return hipGetLastError();
+}
+
+hipError_t launch_probe(ShapeSel sh, int kind, bool nt, int64_t grid, unsigned lds,
+                        hipStream_t st, const CopySeg* s, const PairDesc* p, uint32_t ns,
+                        uint32_t items, uint32_t cpt, uint32_t* sink, uint32_t magic) {
+#define AEGKV_PR(W, UU)                                                                     \
+  if (sh.wg == W && sh.u == UU) {                                                           \
+    if (kind == PROBE_READ)                                                                 \
+      return launch_probe_t<W, UU, PROBE_READ, false>(grid, lds, st, s, p, ns, items, cpt,  \
+                                                      sink, magic);                         \
+    return nt ? launch_probe_t<W, UU, PROBE_WRITE, true>(grid, lds, st, s, p, ns, items,    \
+                                                         cpt, sink, magic)                  \
+              : launch_probe_t<W, UU, PROBE_WRITE, false>(grid, lds, st, s, p, ns, items,   \
+                                                          cpt, sink, magic);                \
+  }
+  AEGKV_PR(256, 1) AEGKV_PR(256, 2) AEGKV_PR(256, 4) AEGKV_PR(256, 8)
+  AEGKV_PR(1024, 1) AEGKV_PR(1024, 2) AEGKV_PR(1024, 3) AEGKV_PR(1024, 4)
+  AEGKV_PR(1024, 5) AEGKV_PR(1024, 6) AEGKV_PR(1024, 8) AEGKV_PR(1024, 10)
+#undef AEGKV_PR
   return hipErrorInvalidValue;
 }
 
@@ -1293,7 +1382,8 @@ struct CopyPlan {
 int copy_plan(const Tunables& t, bool vec, int64_t max_page, int32_t num_segments,
               int64_t num_pairs, CopyPlan* out) {
   ShapeSel sh = auto_shape(max_page);
-  if (t.copy_unroll > 0) sh = ShapeSel{1024, static_cast<int>(t.copy_unroll)};
+  if (t.copy_unroll > 0)
+    sh = ShapeSel{t.copy_lanes == 256 ? 256 : 1024, static_cast<int>(t.copy_unroll)};
   if (!vec) sh = ShapeSel{256, 1};
   const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
   const int64_t items = num_pairs * num_segments * cpt;
@@ -1320,23 +1410,37 @@ void pack_copy_desc(char* h, int32_t num_segments, void* const* src_bases,
   for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_ids[i], dst_ids[i]};
 }
 
-// Launch the copy kernel over descriptors already on the device at `dv`.
+// What a copy call launches: the copy itself, or one of its measurement
+// twins (aegkv_copy_probe) with the sink word and magic they take.
+struct CopyKind {
+  int probe = 0;            // 0 = copy, PROBE_READ or PROBE_WRITE
+  uint32_t* sink = nullptr;
+  uint32_t magic = 0;
+};
+
+// Launch the copy kernel (or a probe twin) over descriptors already on the
+// device at `dv`, with the copy's grid and LDS policy.
 hipError_t copy_launch(const CopyPlan& p, const Tunables& t, int num_cus, int32_t num_segments,
-                       const char* dv, hipStream_t stream) {
-  return launch_copy(p.sh, p.vec, t.nt_stores != 0,
-                     launch_grid(t.copy_wgs_per_cu * num_cus, p.items, p.sh.wg),
-                     p.sh.wg == 1024 && p.sh.chunk() >= (int64_t(32) << 10)
-                         ? static_cast<unsigned>(t.copy_lds_bytes) : 0u,
-                     stream, reinterpret_cast<const CopySeg*>(dv),
-                     reinterpret_cast<const PairDesc*>(dv + copy_pair_offset(num_segments)),
-                     static_cast<uint32_t>(num_segments), static_cast<uint32_t>(p.items),
-                     static_cast<uint32_t>(p.cpt));
+                       const char* dv, hipStream_t stream, const CopyKind& kind = CopyKind()) {
+  const int64_t grid = launch_grid(t.copy_wgs_per_cu * num_cus, p.items, p.sh.wg);
+  const unsigned lds = p.sh.wg == 1024 && p.sh.chunk() >= (int64_t(32) << 10)
+                           ? static_cast<unsigned>(t.copy_lds_bytes) : 0u;
+  const CopySeg* segs = reinterpret_cast<const CopySeg*>(dv);
+  const PairDesc* pairs = reinterpret_cast<const PairDesc*>(dv + copy_pair_offset(num_segments));
+  const uint32_t ns = static_cast<uint32_t>(num_segments);
+  const uint32_t items = static_cast<uint32_t>(p.items);
+  const uint32_t cpt = static_cast<uint32_t>(p.cpt);
+  if (kind.probe)
+    return launch_probe(p.sh, kind.probe, t.nt_stores != 0, grid, lds, stream, segs, pairs, ns,
+                        items, cpt, kind.sink, kind.magic);
+  return launch_copy(p.sh, p.vec, t.nt_stores != 0, grid, lds, stream, segs, pairs, ns, items,
+                     cpt);
 }
 
 int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
               const int64_t* page_bytes, int64_t src_num_blocks, int64_t dst_num_blocks,
               int64_t num_pairs, const int64_t* src_ids, const int64_t* dst_ids, bool same_cache,
-              hipStream_t stream) {
+              hipStream_t stream, const CopyKind& kind = CopyKind()) {
   bool vec = false;
   int64_t max_page = 0;
   int rc = copy_check_layout(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
@@ -1345,6 +1449,9 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   if (!rc) rc = copy_check_ranges(src_num_blocks, dst_num_blocks, num_pairs, src_ids, dst_ids);
   if (!rc) rc = copy_check_ids_map(dst_num_blocks, num_pairs, src_ids, dst_ids, same_cache);
   if (rc || num_pairs == 0) return rc;
+  if (kind.probe && !vec)
+    return fail(AEGKV_EINVAL, "the probes move 16 B per lane: bases and pages must be "
+                "16 B multiples");
   rc = copy_check_device(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
                          dst_num_blocks, same_cache);
   if (rc) return rc;
@@ -1366,12 +1473,12 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   char* dv = ctx->ring.dev + off;
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
-  e = copy_launch(plan, t, ctx->num_cus, num_segments, dv, stream);
+  e = copy_launch(plan, t, ctx->num_cus, num_segments, dv, stream, kind);
   if (e != hipSuccess) {
     // the descriptor upload is already enqueued: retire its region in order
     (void)hipGetLastError();
     (void)ring_commit(ctx->ring, off, total, stream);
-    return hip_fail(e, "copy_blocks_kernel launch");
+    return hip_fail(e, kind.probe ? "copy_probe_kernel launch" : "copy_blocks_kernel launch");
   }
   return ring_commit(ctx->ring, off, total, stream);
 }
@@ -1486,6 +1593,7 @@ int64_t aegkv_tune(int key, int64_t value) {
     case AEGKV_TUNE_NT_STORES: slot = &g_tune.nt_stores; break;
     case AEGKV_TUNE_COPY_WGS_PER_CU: slot = &g_tune.copy_wgs_per_cu; break;
     case AEGKV_TUNE_COPY_UNROLL: slot = &g_tune.copy_unroll; break;
+    case AEGKV_TUNE_COPY_LANES: slot = &g_tune.copy_lanes; break;
     case AEGKV_TUNE_SWAP_SHAPE_AUTO: slot = &g_tune.swap_shape_auto; break;
     case AEGKV_TUNE_SWAP_UNROLL: slot = &g_tune.swap_unroll; break;
     case AEGKV_TUNE_STAGED_WORKGROUPS: slot = &g_tune.staged_workgroups; break;
@@ -1512,6 +1620,15 @@ int64_t aegkv_tune(int key, int64_t value) {
       return fail(AEGKV_EINVAL, "staged workgroups must be in [0, 2^24]");
     if (key == AEGKV_TUNE_SWAP_UNROLL && value != 1 && value != 2 && value != 4)
       return fail(AEGKV_EINVAL, "swap unroll must be 1, 2 or 4");
+    if (key == AEGKV_TUNE_COPY_LANES && value != 0 && value != 256 && value != 1024)
+      return fail(AEGKV_EINVAL, "copy lanes must be 0, 256 or 1024");
+    if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && g_tune.copy_lanes == 256 &&
+        value != 1 && value != 2 && value != 4 && value != 8)
+      return fail(AEGKV_EINVAL, "with 256 copy lanes the unroll must be 0, 1, 2, 4 or 8");
+    if (key == AEGKV_TUNE_COPY_LANES && value == 256 && g_tune.copy_unroll != 0 &&
+        g_tune.copy_unroll != 1 && g_tune.copy_unroll != 2 && g_tune.copy_unroll != 4 &&
+        g_tune.copy_unroll != 8)
+      return fail(AEGKV_EINVAL, "256 copy lanes take an unroll of 1, 2, 4 or 8");
     if (key == AEGKV_TUNE_COPY_UNROLL && value != 0 && !valid_copy_unroll(value))
       return fail(AEGKV_EINVAL, "copy unroll must be 0 (auto) or one of 1,2,3,4,5,6,8,10");
     if (key == AEGKV_TUNE_STAGED_DMA_STREAMS && value > kMaxDmaStreams)
@@ -1588,6 +1705,27 @@ int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
   if (int rc = env_status()) return rc;
   return copy_noalloc(num_segments, segment_bases, segment_page_bytes, device_num_blocks,
                       num_pairs, src_block_ids, dst_block_ids, stream);
+}
+
+int aegkv_copy_probe(int kind, int32_t num_segments, void* const* segment_bases,
+                     const int64_t* segment_page_bytes, int64_t device_num_blocks,
+                     int64_t num_pairs, const int64_t* src_block_ids,
+                     const int64_t* dst_block_ids, uint32_t* sink, uint32_t magic,
+                     hipStream_t stream) {
+  g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
+  if (kind != AEGKV_PROBE_READ && kind != AEGKV_PROBE_WRITE)
+    return fail(AEGKV_EINVAL, "probe kind %d is neither AEGKV_PROBE_READ nor AEGKV_PROBE_WRITE",
+                kind);
+  if (!sink || (reinterpret_cast<uintptr_t>(sink) & 3u))
+    return fail(AEGKV_EINVAL, "the probe's sink must be a 4-byte aligned device word");
+  CopyKind k;
+  k.probe = kind == AEGKV_PROBE_READ ? PROBE_READ : PROBE_WRITE;
+  k.sink = sink;
+  k.magic = magic;
+  return copy_core(num_segments, segment_bases, segment_bases, segment_page_bytes,
+                   device_num_blocks, device_num_blocks, num_pairs, src_block_ids,
+                   dst_block_ids, true, stream, k);
 }
 
 int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,

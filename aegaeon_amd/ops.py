@@ -315,6 +315,31 @@ def copy_blocks(
     _lib.check(_call_on(dev, lambda: lib.aegkv_copy_blocks(*args)))
 
 
+PROBE_READ = _lib.PROBE_READ
+PROBE_WRITE = _lib.PROBE_WRITE
+
+
+def copy_probe(kind: int, segments: Sequence[torch.Tensor], src_block_ids, dst_block_ids,
+               sink: torch.Tensor, *, magic: int = 0x9E3779B9,
+               segment_page_bytes: Sequence[int] | None = None,
+               device_num_blocks: int | None = None,
+               stream: torch.cuda.Stream | None = None) -> None:
+    """Measurement only: the read half (PROBE_READ: load every source tile)
+    or the write half (PROBE_WRITE: store a fixed pattern into every target
+    tile, destroying its contents) of copy_blocks with the same ids, work
+    items and launch shape (aegkv_copy_probe). sink: a device int32/uint32
+    tensor the read probe may write one word of."""
+    if kind not in (PROBE_READ, PROBE_WRITE):
+        raise ValueError(f"unknown probe kind {kind!r}")
+    if sink.device.type != "cuda" or sink.element_size() != 4 or sink.numel() < 1:
+        raise ValueError("sink must be a device tensor of 4-byte words")
+    dev, args, _keep = _copy_call_args(segments, src_block_ids, dst_block_ids,
+                                       segment_page_bytes, device_num_blocks, stream)
+    lib = _lib.load()
+    _lib.check(_call_on(dev, lambda: lib.aegkv_copy_probe(
+        kind, *args[:-1], sink.data_ptr(), int(magic) & 0xFFFFFFFF, args[-1])))
+
+
 #: limits of copy_blocks_noalloc (the fixed descriptor array of libaegkv)
 NOALLOC_MAX_SEGMENTS = 1024
 NOALLOC_MAX_PAIRS = 65536

@@ -68,7 +68,8 @@ def parse():
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
     p.add_argument("--config", default="headline",
-                   choices=["headline", "varlen", "overlap", "refplan", "switch", "serving"],
+                   choices=["headline", "varlen", "overlap", "refplan", "switch", "serving",
+                            "tiles"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
                         "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
                         "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams; "
@@ -76,7 +77,8 @@ def parse():
                         "the reference's per-extent copy_ loop on the same GPU; switch: "
                         "two models' KV swapped out and in at once through the planner, "
                         "swapper and move ledger; serving: a bf16 GEMM loop beside both "
-                        "swaps, for the default and a smaller swap grid")
+                        "swaps, for the default and a smaller swap grid; tiles: copy_blocks "
+                        "by tile size (16-160 KiB) beside its read-only and write-only probes")
     return p.parse_args()
 
 
@@ -177,6 +179,28 @@ def measure_stream_copy(torch, dev, nbytes=4 << 30, reps=3):
         best = max(best, 2 * nbytes / (e0.elapsed_time(e1) / 1e3) / 1e9)
     del a_, b_
     return best
+
+
+def copy_probes(torch, ops, segs, src, dst, nbytes, reps=5):
+    """The copy's two halves on the same tiles with the same launch shape
+    (aegkv_copy_probe): reading every source tile, then writing every target
+    tile (their contents are lost). nbytes = bytes each half moves. Returns
+    the rates and the read+write bound they imply for a copy (2 nbytes in
+    nbytes/read + nbytes/write seconds); average over `reps` launches after
+    one warm-up, timed with HIP events on the launching stream."""
+    sink = torch.zeros(4, dtype=torch.int32, device=segs[0].device)
+    out = {}
+    for name, kind in (("read", ops.PROBE_READ), ("write", ops.PROBE_WRITE)):
+        ops.copy_probe(kind, segs, src, dst, sink)
+        a, b = ev_pair(torch)
+        a.record()
+        for _ in range(reps):
+            ops.copy_probe(kind, segs, src, dst, sink)
+        b.record()
+        b.synchronize()
+        out[name] = nbytes / (a.elapsed_time(b) / 1e3 / reps) / 1e9
+    out["rw_bound"] = 2.0 / (1.0 / out["read"] + 1.0 / out["write"])
+    return out
 
 
 def cpu_baseline(runs: int):
@@ -313,6 +337,68 @@ def bench_varlen(args):
         "link_GBps": {"d2h": round(link["d2h"], 3), "h2d": round(link["h2d"], 3)},
         "bit_exact_round_trip": True,
     }
+
+
+TILE_SHAPES = (   # (name, layers, blocks, kv_heads): tiles of 16 x heads x 128 x 2 bytes
+    ("Qwen2.5-7B 16 KiB tiles", 28, 16384, 4),
+    ("Qwen3-4B 32 KiB tiles", 36, 8192, 8),
+    ("Qwen1.5-MoE 64 KiB tiles", 24, 32768, 16),
+    ("Llama-2-13B 160 KiB tiles", 40, 8192, 40),
+)
+
+
+def bench_tiles(args):
+    """copy_blocks by tile size, beside its read-only and write-only probes
+    on the same tiles: each BASELINE KV shape, pairs = two disjoint seeded
+    halves of the blocks (every block is a source or a target)."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    rows = []
+    for name, layers, blocks, heads in TILE_SHAPES:
+        log(f"tiles: {name}")
+        segs = kv_segments(torch, layers, blocks, heads, 128, torch.bfloat16, dev, 7)
+        tile = 16 * heads * 128 * 2
+        perm = torch.randperm(blocks, generator=torch.Generator().manual_seed(7)).numpy()
+        n = blocks // 2
+        src, dst = perm[:n], perm[n:2 * n]
+        nbytes = n * len(segs) * tile
+        ops.copy_blocks(segs, src, dst)
+        a, b = ev_pair(torch)
+        a.record()
+        for _ in range(args.steps):
+            ops.copy_blocks(segs, src, dst)
+        b.record()
+        b.synchronize()
+        t = a.elapsed_time(b) / 1e3 / args.steps
+        si, di = torch.from_numpy(src).to(dev), torch.from_numpy(dst).to(dev)
+        if not all(torch.equal(x[di], x[si]) for x in segs):
+            raise AssertionError(f"{name}: copy_blocks is not bit-exact")
+        pr = copy_probes(torch, ops, segs, src, dst, nbytes, reps=args.steps)
+        copy = 2 * nbytes / t / 1e9
+        rows.append({"shape": name, "tile_bytes": tile, "segments": len(segs), "pairs": n,
+                     "bytes_rw": 2 * nbytes, "copy_ms": round(t * 1e3, 3),
+                     "copy_GBps": round(copy, 1), "copy_frac_hbm_peak": round(copy / HBM_PEAK_GBPS, 4),
+                     "read_GBps": round(pr["read"], 1), "write_GBps": round(pr["write"], 1),
+                     "rw_bound_GBps": round(pr["rw_bound"], 1),
+                     "copy_frac_of_rw_bound": round(copy / pr["rw_bound"], 4)})
+        del segs
+        torch.cuda.empty_cache()
+    # a plain device copy of known size (4 GiB each way), the calibration
+    # that HBM traffic counters of the kernels above are scaled by
+    a_ = torch.empty(1 << 32, dtype=torch.uint8, device=dev)
+    b_ = torch.empty_like(a_)
+    b_.copy_(a_)
+    torch.cuda.synchronize()
+    del a_, b_
+    return {"metric": "copy_blocks GB/s by tile size (read+write) with read/write probes",
+            "unit": "GB/s", "steps": args.steps, "rows": rows,
+            "calibration": "one torch copy_ of 4294967296 bytes each way at the end"}
 
 
 def bench_overlap(args):
@@ -867,7 +953,8 @@ def main():
         sys.exit(2)
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
-              "switch": bench_switch, "serving": bench_serving}[args.config]
+              "switch": bench_switch, "serving": bench_serving,
+              "tiles": bench_tiles}[args.config]
         print(json.dumps(fn(args)), flush=True)
         return
     import numpy as np
@@ -951,6 +1038,9 @@ def main():
     if not (swap_ok and copy_ok):
         raise AssertionError(f"bit-exact check failed: swap {swap_ok}, copy_blocks {copy_ok}")
 
+    log("read-only and write-only probes over the copy's tiles")
+    probes = copy_probes(torch, ops, segs2, csrc, cdst, copy_bytes // 2)
+
     t_d2h, t_h2d, t_cpy = sum(d2h) / len(d2h), sum(h2d) / len(h2d), sum(cpy) / len(cpy)
     d2h_gbps = swap_bytes / t_d2h / 1e9
     h2d_gbps = swap_bytes / t_h2d / 1e9
@@ -1013,6 +1103,16 @@ def main():
             "frac": round(copy_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "avg_launch_ms": round(t_cpy * 1e3, 3),
+        },
+        "hbm_probes": {
+            "what": ("the copy's halves alone on the same tiles, ids and launch shape "
+                     "(aegkv_copy_probe): read every source tile / write every target tile; "
+                     "a copy of B bytes each way needs at least B/read + B/write seconds"),
+            "hbm_read_GBps": round(probes["read"], 1),
+            "hbm_write_GBps": round(probes["write"], 1),
+            "rw_bound_GBps": round(probes["rw_bound"], 1),
+            "rw_bound_frac_hbm_peak": round(probes["rw_bound"] / HBM_PEAK_GBPS, 4),
+            "copy_frac_of_rw_bound": round(copy_gbps / probes["rw_bound"], 4),
         },
         "link_roofline": {
             "bound": "host-link (measured)",

@@ -97,6 +97,10 @@ extern "C" {
 #define AEGKV_TUNE_SWAP_OUT_WORKGROUPS_UNCACHED 15 /* swap-out kernel into an
                                         uncached pool: workgroups (112)    */
 /* key 16 is retired: aegkv_tune rejects it as an unknown key */
+#define AEGKV_TUNE_COPY_LANES 17     /* copy_blocks with a fixed unroll (key
+                                        7): 256 or 1024 lanes per workgroup
+                                        (0 = 1024; 256 lanes take an unroll
+                                        of 1, 2, 4 or 8)                   */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);
@@ -198,6 +202,25 @@ int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
                               const int64_t* segment_page_bytes, int64_t device_num_blocks,
                               int64_t num_pairs, const int64_t* src_block_ids,
                               const int64_t* dst_block_ids, hipStream_t stream);
+
+/*
+ * Measurement only (no counterpart in the reference): the read half or the
+ * write half of aegkv_copy_blocks on its own. Same arguments, checks, work
+ * items, grid and launch shape as aegkv_copy_blocks; AEGKV_PROBE_READ loads
+ * every source tile (the loads are folded and the fold is stored to *sink
+ * only if it equals `magic`), AEGKV_PROBE_WRITE stores a fixed pattern into
+ * every target tile (their previous contents are lost) and reads nothing.
+ * Their rates bound what a copy over the same tiles can reach: a copy of B
+ * bytes each way takes at least B/read_rate + B/write_rate. Tiles must be
+ * 16 B aligned multiples of 16 B. sink: a 4-byte aligned device word.
+ */
+#define AEGKV_PROBE_READ 1
+#define AEGKV_PROBE_WRITE 2
+int aegkv_copy_probe(int kind, int32_t num_segments, void* const* segment_bases,
+                     const int64_t* segment_page_bytes, int64_t device_num_blocks,
+                     int64_t num_pairs, const int64_t* src_block_ids,
+                     const int64_t* dst_block_ids, uint32_t* sink, uint32_t magic,
+                     hipStream_t stream);
 
 /*
  * Block migration between two caches of the same layout: for every segment

@@ -339,11 +339,42 @@ def restore_tuning():
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
             _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
             _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS, _lib.TUNE_STAGED_OVERLAP,
-            _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED)
+            _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_COPY_LANES)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
         _lib.tune(k, v)
+
+
+@pytest.mark.parametrize("page", [16 * 1024, 64 * 1024, 160 * 1024, 4096, 4000 + 16 * 3])
+def test_copy_probes_touch_only_their_tiles(gpu, page):
+    """The read probe changes nothing; the write probe fills exactly the
+    target tiles with its pattern (third word 0x5a5a5a5a, fourth the magic
+    value) and leaves every other byte alone."""
+    n_seg, n_blocks, n = 6, 96, 30
+    g = torch.Generator(device=gpu).manual_seed(page)
+    segs = [torch.randint(0, 256, (n_blocks, page), dtype=torch.uint8, device=gpu, generator=g)
+            for _ in range(n_seg)]
+    before = [t.clone() for t in segs]
+    rng = np.random.default_rng(page)
+    perm = rng.permutation(n_blocks)
+    src, dst = perm[:n], perm[n:2 * n]
+    sink = torch.zeros(4, dtype=torch.int32, device=gpu)
+    ops.copy_probe(ops.PROBE_READ, segs, src, dst, sink)
+    torch.cuda.synchronize()
+    for a, b in zip(segs, before):
+        assert torch.equal(a, b)
+    magic = 0x12345677
+    ops.copy_probe(ops.PROBE_WRITE, segs, src, dst, sink, magic=magic)
+    torch.cuda.synchronize()
+    di = torch.from_numpy(dst).to(gpu)
+    keep = torch.ones(n_blocks, dtype=torch.bool, device=gpu)
+    keep[di] = False
+    for a, b in zip(segs, before):
+        assert torch.equal(a[keep], b[keep])
+        words = a[di].view(torch.int32).view(n, page // 16, 4)
+        assert bool((words[:, :, 2] == 0x5a5a5a5a).all())
+        assert bool((words[:, :, 3] == magic).all())
 
 
 def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
@@ -353,8 +384,11 @@ def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
     rng = np.random.default_rng(21)
     n = 24
     page = np.array([160 * 1024, 48 * 1024 + 16, 4096, 32 * 1024, 112], np.int64)
-    for unroll, wpc, lds in itertools.product((0, 1, 2, 3, 4, 5, 6, 8, 10), (0, 3),
-                                              (0, 96 * 1024, 160 * 1024)):
+    shapes = [(1024, u) for u in (0, 1, 2, 3, 4, 5, 6, 8, 10)] + [(256, u) for u in (1, 2, 4, 8)]
+    for (lanes, unroll), wpc, lds in itertools.product(shapes, (0, 3),
+                                                       (0, 96 * 1024, 160 * 1024)):
+        _lib.tune(_lib.TUNE_COPY_UNROLL, 0)
+        _lib.tune(_lib.TUNE_COPY_LANES, lanes)
         _lib.tune(_lib.TUNE_COPY_UNROLL, unroll)
         _lib.tune(_lib.TUNE_COPY_WGS_PER_CU, wpc)
         _lib.tune(_lib.TUNE_COPY_LDS_BYTES, lds)
@@ -366,7 +400,7 @@ def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
         oracle.copy_blocks([x.reshape(-1) for x in segs_np], page[:4], n, src, dst)
         torch.cuda.synchronize()
         for s in range(4):
-            assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (unroll, wpc, lds, s)
+            assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (lanes, unroll, wpc, lds, s)
 
 
 @pytest.mark.parametrize("shape_auto,unroll", [(0, 4), (0, 2), (0, 1), (1, 4)])

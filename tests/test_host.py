@@ -429,6 +429,19 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_STAGED_WORKGROUPS) == 0
     assert _lib.tune(_lib.TUNE_STAGED_OVERLAP) == 3
     assert _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED) == 112
+    assert _lib.tune(_lib.TUNE_COPY_LANES) == 0
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_COPY_LANES, 512)
+    assert _lib.tune(_lib.TUNE_COPY_UNROLL, 10) == 0
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_COPY_LANES, 256)           # 256 lanes have no unroll of 10
+    assert _lib.tune(_lib.TUNE_COPY_UNROLL, 0) == 10
+    assert _lib.tune(_lib.TUNE_COPY_LANES, 256) == 0
+    with pytest.raises(ValueError):
+        _lib.tune(_lib.TUNE_COPY_UNROLL, 5)
+    assert _lib.tune(_lib.TUNE_COPY_UNROLL, 8) == 0
+    assert _lib.tune(_lib.TUNE_COPY_UNROLL, 0) == 8
+    assert _lib.tune(_lib.TUNE_COPY_LANES, 0) == 256
     with pytest.raises(ValueError, match="unknown tuning key 16"):
         _lib.tune(16)          # the retired library-driven DMA key
     with pytest.raises(ValueError):
@@ -558,6 +571,31 @@ def test_copy_blocks_noalloc_checks_agree_with_copy_blocks(aegkv_lib):
                                            None)
             assert rc == want, (entry, src.tolist(), dst.tolist(), blocks)
     assert seen == {-2, -3, -5}
+
+
+def test_copy_probe_rejections_before_any_hip_call(aegkv_lib):
+    import numpy as np
+
+    from aegaeon_amd import _lib
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+    bases = (ctypes.c_void_p * 1)(0x10000)
+    page = np.array([4096], np.int64)
+    s, d = np.array([1], np.int64), np.array([2], np.int64)
+
+    def call(kind, sink=0x20000, pg=page, src=s, dst=d):
+        return aegkv_lib.aegkv_copy_probe(kind, 1, bases, pg.ctypes.data_as(P64), 8, src.size,
+                                          src.ctypes.data_as(P64), dst.ctypes.data_as(P64),
+                                          sink, 7, None)
+
+    assert call(0) == _lib.EINVAL
+    assert call(3) == _lib.EINVAL
+    assert call(_lib.PROBE_READ, sink=None) == _lib.EINVAL
+    assert call(_lib.PROBE_WRITE, sink=0x20002) == _lib.EINVAL
+    assert call(_lib.PROBE_READ, pg=np.array([4000 + 8], np.int64)) == _lib.EINVAL  # not 16 B
+    assert b"16 B" in aegkv_lib.aegkv_last_error()
+    assert call(_lib.PROBE_WRITE, dst=np.array([1], np.int64)) == _lib.EOVERLAP
+    assert call(_lib.PROBE_READ, src=np.array([], np.int64), dst=np.array([], np.int64)) == 0
 
 
 def test_copy_blocks_noalloc_limits(aegkv_lib):
