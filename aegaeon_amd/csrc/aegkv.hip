@@ -59,7 +59,10 @@ namespace {
 
 #define fail aegkv_set_error
 
+// Report a failed HIP call and clear the runtime's last-error state, which
+// would otherwise make a later launch check report this failure again.
 int hip_fail(hipError_t e, const char* what) {
+  (void)hipGetLastError();
   return fail(static_cast<int>(e), "%s failed: %s (%d)", what, hipGetErrorString(e),
               static_cast<int>(e));
 }
@@ -634,6 +637,7 @@ struct SwapArgs {
 
 template <int WG, int U, bool TO_HOST, bool VEC, bool NT>
 hipError_t launch_swap_t(int64_t grid, hipStream_t st, const SwapArgs& a) {
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL((swap_tiles_kernel<WG, U, TO_HOST, VEC, NT>),
                      dim3(static_cast<uint32_t>(grid)), dim3(WG), 0, st, a.segs, a.ents, a.kpp,
                      a.num_segs, a.num_items, a.cpt, a.host_base, a.host_stride,
@@ -670,6 +674,7 @@ hipError_t launch_swap(ShapeSel sh, bool to_host, bool vec, bool nt, int64_t gri
 template <int WG, int U, bool VEC, bool NT>
 hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const CopySeg* s,
                          const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL((copy_blocks_kernel<WG, U, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
                      dim3(WG), lds, st, s, p, ns, items, cpt);
   return hipGetLastError();
@@ -694,6 +699,7 @@ template <int WG, int U, int KIND, bool NT>
 hipError_t launch_probe_t(int64_t grid, unsigned lds, hipStream_t st, const CopySeg* s,
                           const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt,
                           uint32_t* sink, uint32_t magic) {
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL((copy_probe_kernel<WG, U, KIND, NT>), dim3(static_cast<uint32_t>(grid)),
                      dim3(WG), lds, st, s, p, ns, items, cpt, sink, magic);
   return hipGetLastError();
@@ -1795,10 +1801,13 @@ int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags) {
   const size_t n = static_cast<size_t>(bytes);
   void* p = nullptr;
   if (flags & AEGKV_HOST_UNCACHED) {
-    // reuse the smallest parked uncached pool that fits and wastes at most a quarter
+    // Reuse the smallest parked uncached pool that fits. Parked memory stays
+    // pinned until the process ends anyway, so a larger one costs nothing
+    // extra, and reusing it keeps the process under the host's cap on pinned
+    // memory when pools of different sizes come and go.
     std::lock_guard<std::mutex> lk(g_host_mu);
     auto it = g_parked.lower_bound(n);
-    if (it != g_parked.end() && it->first - n <= n / 4) {
+    if (it != g_parked.end()) {
       p = reinterpret_cast<void*>(it->second);
       g_parked.erase(it);
     }

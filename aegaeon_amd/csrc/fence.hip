@@ -44,7 +44,10 @@ namespace {
 
 #define fail aegkv_set_error
 
+// Report a failed HIP call and clear the runtime's last-error state, which
+// would otherwise make a later launch check report this failure again.
 int hip_fail(hipError_t e, const char* what) {
+  (void)hipGetLastError();
   return fail(static_cast<int>(e), "%s failed: %s (%d)", what, hipGetErrorString(e),
               static_cast<int>(e));
 }
@@ -184,6 +187,7 @@ int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream) {
   aegkv_clear_error();
   int rc = check_word(word, "fence word");
   if (rc) return rc;
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL(fence_signal_kernel, dim3(1), dim3(64), 0, stream, word, value);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fence_signal_kernel launch");
@@ -205,6 +209,7 @@ int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
   if (rc) return rc;
   // ticks = us * (kHz / 1000); both factors are bounded, no overflow
   const uint64_t budget = static_cast<uint64_t>(timeout_us) * static_cast<uint64_t>(khz) / 1000u;
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL(fence_wait_kernel, dim3(1), dim3(64), 0, stream, word, value, budget,
                      timed_out);
   hipError_t e = hipGetLastError();

@@ -117,22 +117,23 @@ def measure_link_bidir(torch, ops, dev, nbytes=4 << 30, retries=6):
     """Both directions at once, aggregate GB/s: a D2H and an H2D runtime
     copy started together on two streams with hardware queues of their own
     (on streams that share a queue the copies run one after the other);
-    best of three runs.
+    best of three runs. Returns (ceiling, attempts).
 
     Right after another GPU process has exited (a test run, say), the two
     copies were seen running one after the other for some seconds (60 GB/s
     instead of 97) while its queues were still being released; a result
     below 1.25x one direction is measured again after 5 s, up to `retries`
-    times."""
-    best = _bidir_once(torch, ops, dev, nbytes)
+    times. Every attempt is returned, so the record shows when that
+    happened."""
+    attempts = [_bidir_once(torch, ops, dev, nbytes)]
     for _ in range(retries):
-        if best > 1.25 * 57.0:
+        if max(attempts) > 1.25 * 57.0:
             break
-        log(f"bidirectional copies ran one after the other ({best:.1f} GB/s); "
+        log(f"bidirectional copies ran one after the other ({attempts[-1]:.1f} GB/s); "
             "measuring again in 5 s")
         time.sleep(5)
-        best = max(best, _bidir_once(torch, ops, dev, nbytes))
-    return best
+        attempts.append(_bidir_once(torch, ops, dev, nbytes))
+    return max(attempts), [round(x, 3) for x in attempts]
 
 
 def _bidir_once(torch, ops, dev, nbytes):
@@ -204,8 +205,9 @@ def copy_probes(torch, ops, segs, src, dst, nbytes, reps=5):
 
 
 def cpu_baseline(runs: int):
-    """The reference's torch path on host tensors (oracle restatement)."""
-    import numpy as np
+    """The reference's torch path on host tensors (oracle restatement), timed
+    with one torch thread (the stated baseline) and with torch's default
+    thread count."""
     import torch
 
     from oracle import oracle
@@ -225,34 +227,41 @@ def cpu_baseline(runs: int):
     owners = [{0}] * S
     cpu_off = [s * tile for s in range(S)]
     z, one = [0] * n, [1] * n
-    threads = torch.get_num_threads()
-    torch.set_num_threads(1)  # the timed loop: one thread (extents sit at torch's grain size)
-    times = []
-    for r in range(runs + 1):
-        t0 = time.perf_counter()
-        oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite, src,
-                                 list(range(n)), z, z, one, False)
-        oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite,
-                                 list(range(n)), dst, z, z, one, True)
-        dt = time.perf_counter() - t0
-        if r:
-            times.append(dt)
+    default_threads = torch.get_num_threads()
+    moved = 2 * n * composite
+    rates = {}
+    for threads in (1, default_threads):
+        torch.set_num_threads(threads)
+        times = []
+        for r in range(runs + 1):
+            t0 = time.perf_counter()
+            oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite, src,
+                                     list(range(n)), z, z, one, False)
+            oracle.swap_blocks_torch(pages, staging, cpu_off, owners, [1], 0, composite,
+                                     list(range(n)), dst, z, z, one, True)
+            dt = time.perf_counter() - t0
+            if r:
+                times.append(dt)
+        rates[threads] = moved / statistics.median(times) / 1e9
+    torch.set_num_threads(default_threads)
     idx_s, idx_d = torch.tensor(src), torch.tensor(dst)
     ok = all(torch.equal(p[idx_d], p[idx_s]) for p in pages)
     if not ok:
         raise AssertionError("CPU baseline round trip is not bit-exact")
-    torch.set_num_threads(threads)
-    t = statistics.median(times)
-    moved = 2 * n * composite
     return {
-        "value": round(moved / t / 1e9, 3),
+        "value": round(rates[1], 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
+        "default_threads": default_threads,
+        "value_default_threads": round(rates[default_threads], 3),
+        "os_cpu_count": os.cpu_count(),
         "sample": (f"reference torch path (per-extent narrow().copy_(), worker.py:2272-2328) on "
                    f"host tensors: 72 x [2048,16,8,128] bf16 N(0,1); gather 256 blocks to "
-                   f"staging + scatter to 256 other ids = {moved} bytes; median of {runs} runs, "
-                   f"torch threads 1 of os.cpu_count()={os.cpu_count()}; bit-exact round trip"),
+                   f"staging + scatter to 256 other ids = {moved} bytes; median of {runs} runs "
+                   f"each with torch threads 1 (value) and {default_threads} "
+                   f"(value_default_threads), os.cpu_count()={os.cpu_count()}; bit-exact "
+                   f"round trip"),
     }
 
 
@@ -419,7 +428,7 @@ def bench_overlap(args):
     masks = ([ops.xcd_cu_mask(8, device=dev)] * 2 + [ops.xcd_cu_mask(24, 8, device=dev)]
              if partition else [None] * 3)
     owners = [ops.DedicatedStream(dev, m) for m in masks]
-    bidir = measure_link_bidir(torch, ops, dev)
+    bidir = getattr(args, "bidir", None) or measure_link_bidir(torch, ops, dev)[0]
     L, NB, H, D = 24, 32768, 16, 128
     NOUT, NIN, NP = 16384, 12288, 2048
     segs = kv_segments(torch, L, NB, H, D, torch.bfloat16, dev, 4)
@@ -427,15 +436,20 @@ def bench_overlap(args):
     tile = 16 * H * D * 2
     page = S * tile
     # 28,672 host pages need 84 GiB of pinned memory; hosts that cap pinned
-    # memory lower run the same shape with 3/4 of the swapped blocks.
-    scale = 1.0
-    try:
-        pool = ops.PinnedHostPool((NOUT + NIN) * page, uncached=True)
-    except _lib.AegkvError:
-        scale = 0.75
-        NOUT, NIN = int(NOUT * scale), int(NIN * scale)
-        pool = ops.PinnedHostPool((NOUT + NIN) * page, uncached=True)
-        log(f"pinned pool capped: running swap-out {NOUT}, swap-in {NIN} blocks")
+    # memory lower (these pin 63 GiB but not 84) run the same shape with 7/8
+    # or 3/4 of the swapped blocks.
+    pool = None
+    for scale in (1.0, 0.875, 0.75):
+        try:
+            pool = ops.PinnedHostPool((int(NOUT * scale) + int(NIN * scale)) * page,
+                                      uncached=True)
+            break
+        except _lib.AegkvError as exc:
+            log(f"pinned pool at swap scale {scale} refused: {exc}")
+    if pool is None:
+        raise RuntimeError("no pinned pool for the overlap config, even at 3/4 scale")
+    NOUT, NIN = int(NOUT * scale), int(NIN * scale)
+    log(f"overlap: swap-out {NOUT}, swap-in {NIN} blocks (scale {scale})")
     rng = np.random.default_rng(4)
     perm = rng.permutation(NB)
     out_ids, in_ids = perm[:NOUT], perm[NOUT:NOUT + NIN]
@@ -496,7 +510,12 @@ def bench_overlap(args):
     if not (ok_in and ok_cp and ok_out):
         raise AssertionError(f"overlap check failed: in {ok_in} copy {ok_cp} out {ok_out}")
     b_out, b_in, b_cp = NOUT * page, NIN * page, 2 * NP * page
+    del lay, pages
     pool.free()
+    del segs
+    for o in owners:
+        o.close()
+    torch.cuda.empty_cache()
     return {
         "metric": "KV swap + copy_blocks GB/s, three streams at once",
         "unit": "GB/s",
@@ -544,7 +563,7 @@ def bench_switch(args):
     _lib.load()
     bidir = getattr(args, "bidir", None)
     if bidir is None:   # measured before the swappers create their streams
-        bidir = measure_link_bidir(torch, ops, dev)
+        bidir = measure_link_bidir(torch, ops, dev)[0]
     L, NB, H, D, NREQ = 28, 16384, 4, 128, 64
     specs = kv_tensor_specs(L, NB, 16, H, D, 2)
     names = [{f"layers.{l}.{kv}" for l in range(L) for kv in ("k", "v")}]
@@ -967,9 +986,10 @@ def main():
     _lib.load()
 
     log("measuring host-link and stream-copy ceilings")
-    bidir = None if args.no_switch else measure_link_bidir(torch, ops, dev)
+    bidir, bidir_attempts = measure_link_bidir(torch, ops, dev)
     link = measure_link(torch, ops, dev)
     stream_copy = measure_stream_copy(torch, dev)
+
 
     # ---- Qwen3-4B swap workload
     log("allocating Qwen3-4B KV cache and pinned pool")
@@ -1128,6 +1148,10 @@ def main():
             "avg_launch_ms_h2d": round(t_h2d * 1e3, 3),
         },
     }
+    line["link_bidirectional"] = {
+        "ceiling_GBps": round(bidir, 3), "attempts_GBps": bidir_attempts,
+        "what": "a D2H and an H2D 4 GiB runtime copy at once on two dedicated streams, best "
+                "of 3 per attempt; an attempt below 1.25x one direction is repeated after 5 s"}
     # The reference's own data path on this GPU: Worker.swap_blocks' loop of
     # one copy_(non_blocking=True) per (segment, block) tile, same blocks.
     line["reference_path_same_gpu"] = None

@@ -316,8 +316,9 @@ int aegkv_host_alloc(void** ptr, int64_t bytes);
  * both directions at once 87 -> 90 GB/s; a blit hipMemcpyAsync is
  * unchanged. Such a pool is never returned to the runtime before the
  * process ends: aegkv_host_free parks it, and a later uncached allocation
- * whose size it fits (wasting at most a quarter) reuses it. Meant for
- * long-lived pools such as a KV host pool.
+ * that it fits reuses it (the smallest such parked pool), which keeps a
+ * process whose pools come and go under the host's cap on pinned memory.
+ * Meant for long-lived pools such as a KV host pool.
  */
 #define AEGKV_HOST_UNCACHED 1
 int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags);
