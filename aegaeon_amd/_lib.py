@@ -62,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "aegkv_copy_blocks_noalloc",
     "aegkv_copy_probe",
     "aegkv_migrate_blocks",
+    "aegkv_load_slices",
     "aegkv_transfer_entries",
     "aegkv_host_alloc",
     "aegkv_host_alloc_flags",
@@ -99,6 +100,7 @@ _SIGNATURES = {
     "aegkv_copy_probe": (_INT, [_INT, _I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P,
                                 ctypes.c_uint32, _P]),
     "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_load_slices": (_INT, [_I64, _PP, _PP, _I64P, _INT, _P]),
     "aegkv_transfer_entries": (
         _INT,
         [_I32, _I32P, _I64P, _I64P, _I64P, _I64, _I64P, _I64P, _I64P, _I64, _I64P, _I32P,

@@ -374,6 +374,44 @@ __global__ __launch_bounds__(WG) void copy_probe_kernel(
   }
 }
 
+// One contiguous slice of a weight load: `bytes` bytes from src to dst; its
+// work items start at first_item.
+struct SliceDesc {
+  char* dst;
+  const char* src;
+  int64_t bytes;
+  int64_t first_item;
+};
+static_assert(sizeof(SliceDesc) == 32, "SliceDesc layout");
+
+// Contiguous slices, host to device (weight loads): item w -> the slice
+// that holds it (the last one whose first_item <= w, found by a binary
+// search over the uniform descriptor) and its chunk in that slice. Empty
+// slices are dropped on the host, so every slice has at least one item.
+template <int WG, int U, bool VEC, bool NT_STORE>
+__global__ __launch_bounds__(WG) void slices_kernel(const SliceDesc* __restrict__ slices,
+                                                    uint32_t num_slices, uint32_t num_items) {
+  constexpr int64_t kChunk = Shape<WG, U>::kChunk;
+  for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
+    uint32_t lo = 0, hi = num_slices - 1;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (slices[mid].first_item <= static_cast<int64_t>(w))
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const SliceDesc sl = slices[lo];
+    const int64_t begin = (static_cast<int64_t>(w) - sl.first_item) * kChunk;
+    const uint32_t nbytes =
+        static_cast<uint32_t>((sl.bytes - begin < kChunk) ? (sl.bytes - begin) : kChunk);
+    if (VEC)
+      move_chunk16<WG, U, NT_STORE>(sl.src + begin, sl.dst + begin, nbytes);
+    else
+      move_chunk_bytes<WG>(sl.src + begin, sl.dst + begin, nbytes);
+  }
+}
+
 // Shapes the library instantiates. 1024-lane shapes move 16 KiB rows; a
 // tile that is a multiple of 16 KiB gets the largest U dividing its row
 // count, so one workgroup moves a whole tile (up to 160 KiB) with no tail
@@ -723,6 +761,22 @@ hipError_t launch_probe(ShapeSel sh, int kind, bool nt, int64_t grid, unsigned l
   AEGKV_PR(1024, 5) AEGKV_PR(1024, 6) AEGKV_PR(1024, 8) AEGKV_PR(1024, 10)
 #undef AEGKV_PR
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_slices(bool vec, bool nt, int64_t grid, hipStream_t st,
+                         const SliceDesc* slices, uint32_t num_slices, uint32_t items) {
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
+  const dim3 g(static_cast<uint32_t>(grid));
+  if (!vec)
+    hipLaunchKernelGGL((slices_kernel<256, 1, false, false>), g, dim3(256), 0, st, slices,
+                       num_slices, items);
+  else if (nt)
+    hipLaunchKernelGGL((slices_kernel<256, 2, true, true>), g, dim3(256), 0, st, slices,
+                       num_slices, items);
+  else
+    hipLaunchKernelGGL((slices_kernel<256, 2, true, false>), g, dim3(256), 0, st, slices,
+                       num_slices, items);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------ swap core --
@@ -1576,6 +1630,89 @@ int copy_noalloc(int32_t num_segments, void* const* bases, const int64_t* page_b
   return 0;
 }
 
+// Weight slices host -> device in one call (aegkv_load_slices).
+int slices_core(int64_t n, void* const* dst, const void* const* src, const int64_t* bytes,
+                int mode, hipStream_t stream) {
+  if (n < 0) return fail(AEGKV_EINVAL, "num_slices must be >= 0");
+  if (n > 0 && (!dst || !src || !bytes)) return fail(AEGKV_EINVAL, "slice arrays must not be null");
+  if (mode < AEGKV_MODE_AUTO || mode > AEGKV_MODE_STAGED)
+    return fail(AEGKV_EINVAL, "unknown transfer mode %d", mode);
+  const Tunables t = tunables();
+  if (mode == AEGKV_MODE_AUTO) mode = static_cast<int>(t.auto_h2d);
+  // non-empty slices, checked; distinct targets
+  std::vector<int64_t> keep;
+  keep.reserve(static_cast<size_t>(n));
+  bool vec = true;
+  for (int64_t i = 0; i < n; ++i) {
+    if (bytes[i] < 0)
+      return fail(AEGKV_EINVAL, "slice %lld has %lld bytes", static_cast<long long>(i),
+                  static_cast<long long>(bytes[i]));
+    if (bytes[i] == 0) continue;
+    if (!dst[i] || !src[i])
+      return fail(AEGKV_EINVAL, "slice %lld has a null pointer", static_cast<long long>(i));
+    keep.push_back(i);
+    vec = vec && aligned16(dst[i]) && aligned16(src[i]) && bytes[i] % 16 == 0;
+  }
+  std::vector<int64_t> by_dst(keep);
+  std::sort(by_dst.begin(), by_dst.end(), [&](int64_t a, int64_t b) {
+    return reinterpret_cast<uintptr_t>(dst[a]) < reinterpret_cast<uintptr_t>(dst[b]);
+  });
+  for (size_t k = 1; k < by_dst.size(); ++k) {
+    const int64_t a = by_dst[k - 1], b = by_dst[k];
+    if (reinterpret_cast<uintptr_t>(dst[a]) + static_cast<uint64_t>(bytes[a]) >
+        reinterpret_cast<uintptr_t>(dst[b]))
+      return fail(AEGKV_EOVERLAP, "target slices %lld and %lld overlap",
+                  static_cast<long long>(a), static_cast<long long>(b));
+  }
+  if (keep.empty()) return 0;
+  for (int64_t i : keep) {
+    int rc = check_device_range(dst[i], bytes[i], "target slice");
+    if (!rc) rc = check_host_range(src[i], bytes[i], "source slice");
+    if (rc) return rc;
+  }
+  if (mode == AEGKV_MODE_STAGED) {
+    // the runtime's DMA copy per slice, as the reference's copy_ per slice
+    for (int64_t i : keep)
+      AEGKV_HIP(hipMemcpyAsync(dst[i], src[i], static_cast<size_t>(bytes[i]),
+                               hipMemcpyHostToDevice, stream));
+    return 0;
+  }
+  const int64_t chunk = vec ? int64_t(256) * 16 * 2 : int64_t(256) * 16;
+  int64_t items = 0;
+  for (int64_t i : keep) items += (bytes[i] + chunk - 1) / chunk;
+  if (items >= (int64_t(1) << 32) || keep.size() >= (size_t(1) << 32))
+    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
+                static_cast<long long>(items));
+  DeviceCtx* ctx = nullptr;
+  int rc = get_ctx(&ctx);
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const size_t total = sizeof(SliceDesc) * keep.size();
+  size_t off = 0;
+  rc = ring_reserve(ctx->ring, total, &off);
+  if (rc) return rc;
+  SliceDesc* h = reinterpret_cast<SliceDesc*>(ctx->ring.host + off);
+  int64_t first = 0;
+  for (size_t k = 0; k < keep.size(); ++k) {
+    const int64_t i = keep[k];
+    h[k] = SliceDesc{static_cast<char*>(dst[i]), static_cast<const char*>(src[i]), bytes[i],
+                     first};
+    first += (bytes[i] + chunk - 1) / chunk;
+  }
+  char* dv = ctx->ring.dev + off;
+  hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
+  e = launch_slices(vec, t.nt_stores != 0, launch_grid(t.swap_in_workgroups, items, 256), stream,
+                    reinterpret_cast<const SliceDesc*>(dv), static_cast<uint32_t>(keep.size()),
+                    static_cast<uint32_t>(items));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)ring_commit(ctx->ring, off, total, stream);
+    return hip_fail(e, "slices_kernel launch");
+  }
+  return ring_commit(ctx->ring, off, total, stream);
+}
+
 }  // namespace
 
 // =============================================================== C ABI ==
@@ -1746,6 +1883,13 @@ int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
   return copy_core(num_segments, src_segment_bases, dst_segment_bases, segment_page_bytes,
                    src_num_blocks, dst_num_blocks, num_pairs, src_block_ids, dst_block_ids,
                    false, stream);
+}
+
+int aegkv_load_slices(int64_t num_slices, void* const* dst, const void* const* src,
+                      const int64_t* bytes, int mode, hipStream_t stream) {
+  g_err[0] = '\0';
+  if (int rc = env_status()) return rc;
+  return slices_core(num_slices, dst, src, bytes, mode, stream);
 }
 
 int aegkv_stream_create(hipStream_t* stream) {

@@ -366,6 +366,40 @@ def copy_blocks_noalloc(
     _lib.check(_call_on(dev, lambda: lib.aegkv_copy_blocks_noalloc(*args)))
 
 
+def load_slices(dst: Sequence[torch.Tensor], src: Sequence[torch.Tensor], *, mode="auto",
+                stream: torch.cuda.Stream | None = None) -> None:
+    """dst[i] <- src[i] byte for byte for every i, pinned host -> device, in
+    one aegkv_load_slices call: the weight load of a model switch, where the
+    reference runs one `slice_storage.copy_(tensors_storage,
+    non_blocking=True)` per tensors content
+    (aegaeon/loader/quick_loader.py:325-340). mode "direct" (and "auto"):
+    one kernel reads the host memory over PCIe; "staged": one runtime DMA
+    copy per slice. Runs on `stream` (default: the current stream of dst's
+    device)."""
+    if len(dst) != len(src):
+        raise ValueError(f"{len(dst)} target slices for {len(src)} source slices")
+    if not dst:
+        return
+    dev = dst[0].device
+    sizes = []
+    for i, (d, h) in enumerate(zip(dst, src)):
+        _require_device(d, f"target slice {i}")
+        _require_host(h, f"source slice {i}")
+        if d.device != dev:
+            raise ValueError("all target slices must live on one device")
+        if _tensor_bytes(d) != _tensor_bytes(h):
+            raise ValueError(f"slice {i}: {_tensor_bytes(h)} source bytes for "
+                             f"{_tensor_bytes(d)} target bytes")
+        sizes.append(_tensor_bytes(d))
+    n = len(dst)
+    d_ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in dst])
+    s_ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in src])
+    b = np.ascontiguousarray(np.array(sizes, np.int64))
+    lib = _lib.load()
+    _lib.check(_call_on(dev, lambda: lib.aegkv_load_slices(
+        n, d_ptrs, s_ptrs, _p64(b), _mode(mode), _stream_ptr(dev, stream))))
+
+
 def migrate_blocks(
     src_segments: Sequence[torch.Tensor],
     dst_segments: Sequence[torch.Tensor],

@@ -60,6 +60,11 @@ def parse():
     p.add_argument("--cpu-runs", type=int, default=5)
     p.add_argument("--no-serving", action="store_true",
                    help="skip the serving line (swaps beside a GEMM loop)")
+    p.add_argument("--weight-mode", default="auto", choices=["auto", "direct", "staged"],
+                   help="switch config: how the incoming model's weights are loaded "
+                        "(kernel over PCIe or the runtime's DMA per content)")
+    p.add_argument("--no-weights", dest="weights", action="store_false",
+                   help="switch config: KV swaps only, no weight loads")
     p.add_argument("--no-cu-partition", action="store_true",
                    help="overlap config: run the three streams on every CU")
     p.add_argument("--no-side-by-side", action="store_true",
@@ -637,6 +642,48 @@ def bench_switch(args):
         if it >= args.warmup:
             runs.append((t2 - t0, t1 - t0, b_out, b_in))
         active = 1 - active
+    # The same switches with the incoming model's weights loaded too (one
+    # Qwen2.5-7B bf16 model, 30 contents, 15.2 GB, pinned on the host): on
+    # the incoming swap-in stream before its KV swap-in, as Worker.switch
+    # loads the model before the KV cache (worker.py:455-551). The weights
+    # share the host-to-device direction with the KV swap-in.
+    wruns = []
+    w_bytes = 0
+    link = getattr(args, "link", None)
+    if getattr(args, "weights", True):
+        from aegaeon_amd import weights as wmod
+
+        sizes = wmod.qwen2_content_bytes()
+        host_w = wmod.HostWeights(sizes, uncached=True)
+        g8 = torch.Generator(device=dev).manual_seed(8)
+        for h in host_w.slices:
+            h.copy_(torch.randint(0, 256, (h.numel(),), dtype=torch.uint8, device=dev,
+                                  generator=g8))
+        dev_w = wmod.DeviceWeights(sizes, dev)
+        w_bytes = host_w.total_bytes
+        torch.cuda.synchronize()
+        if link is None:
+            link = measure_link(torch, ops, dev)
+        wmode = getattr(args, "weight_mode", "auto")
+        for it in range(1 + args.steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            ev_out, b_out = move(active, BLOCK_LOCATION_CPU)
+            wmod.load_model(dev_w, host_w, mode=wmode, stream=sw[1 - active].swap_in_stream)
+            ev_in, b_in = move(1 - active, 1 - active)
+            ev_out.synchronize()
+            ev_in.synchronize()
+            t2 = time.perf_counter()
+            pools.reclaim_gpu_moves(active, wait=False)
+            pools.reclaim_cpu_moves(shape, wait=False)
+            if it >= 1:
+                wruns.append((t2 - t0, b_out, b_in))
+            active = 1 - active
+        w_ok = all(torch.equal(d, h.to(dev)) for d, h in zip(dev_w.slices, host_w.slices))
+        if not w_ok:
+            raise AssertionError("weights loaded during the switch differ from the host copy")
+        del dev_w
+        host_w.free()
     # bring everything back to its own engine and compare with the copies
     for e in range(2):
         if tables[reqs[e][0][0]].location != e:
@@ -652,10 +699,31 @@ def bench_switch(args):
     wall = statistics.median(r[0] for r in runs)
     host_ms = statistics.median(r[1] for r in runs) * 1e3
     moved = statistics.median(r[2] + r[3] for r in runs)
+    with_weights = None
+    if wruns:
+        w_wall = statistics.median(r[0] for r in wruns)
+        w_out = statistics.median(r[1] for r in wruns)
+        w_in = statistics.median(r[2] for r in wruns)
+        bound = max(w_out / (link["d2h"] * 1e9), (w_in + w_bytes) / (link["h2d"] * 1e9))
+        with_weights = {
+            "what": ("the same switches plus the incoming model's weights (Qwen2.5-7B bf16, 30 "
+                     "contents) loaded with aegkv_load_slices on the incoming swap-in stream "
+                     "before its KV swap-in"),
+            "weight_bytes": w_bytes, "weight_mode": getattr(args, "weight_mode", "auto"),
+            "switch_wall_ms": round(w_wall * 1e3, 3),
+            "bytes_per_switch": {"kv_d2h": int(w_out), "kv_h2d": int(w_in), "weights_h2d": w_bytes},
+            "h2d_GBps": round((w_in + w_bytes) / w_wall / 1e9, 3),
+            "d2h_GBps": round(w_out / w_wall / 1e9, 3),
+            "link_bound_ms": round(bound * 1e3, 3),
+            "frac_link_bound": round(bound / w_wall, 4),
+            "link_bound": "max(KV out / measured D2H link, (KV in + weights) / measured H2D link)",
+            "bit_exact": True,
+        }
     for s in sw:
         s.close()
     host.free()
     return {
+        "with_weights": with_weights,
         "metric": "model-switch wall time and link rate through planner + swapper + ledger",
         "unit": "GB/s",
         "config": {"workload": "two Qwen2.5-7B KV caches (56 x [16384,16,4,128] bf16 each), "
@@ -1213,11 +1281,12 @@ def main():
     line["model_switch"] = None
     if not args.no_switch:
         log("model switch: two engines, swap-out and swap-in at once")
-        sw = bench_switch(argparse.Namespace(steps=5, warmup=1, bidir=bidir))
+        sw = bench_switch(argparse.Namespace(steps=5, warmup=1, bidir=bidir, link=link,
+                                             weights=True, weight_mode="auto"))
         line["model_switch"] = {k: sw[k] for k in (
             "switch_wall_ms", "host_plan_and_enqueue_ms", "bytes_per_switch",
             "link_aggregate_GBps", "link_bidirectional_ceiling_GBps",
-            "frac_bidirectional_ceiling", "bit_exact")}
+            "frac_bidirectional_ceiling", "bit_exact", "with_weights")}
         line["model_switch"]["workload"] = sw["config"]["workload"]
         torch.cuda.empty_cache()
     # Swaps beside model compute (see --config serving): DIRECT or STAGED

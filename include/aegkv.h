@@ -246,6 +246,23 @@ int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
                          hipStream_t stream);
 
 /*
+ * Weight load on a model switch: num_slices contiguous slices, pinned host
+ * -> device, dst[i][0, bytes[i]) <- src[i][0, bytes[i]), in one call.
+ * Replaces QuickLoader.load_tensors_content's one
+ * `slice_storage.copy_(tensors_content.tensors_storage, non_blocking=True)`
+ * per tensors content (aegaeon/loader/quick_loader.py:325-340), looped over
+ * a model's sharding contents by load_model_to_tensors (:297-323) inside
+ * Worker.switch (aegaeon/worker.py:455-551). mode DIRECT (and AUTO when it
+ * resolves to DIRECT for swap-in): one kernel reads the pinned host memory
+ * over PCIe (16 B per lane when every pointer and size is a 16 B multiple);
+ * mode STAGED: one hipMemcpyAsync per slice, the runtime's DMA copy. Target
+ * slices must not overlap (AEGKV_EOVERLAP); sources must be pinned host
+ * memory and targets device memory; empty slices are skipped.
+ */
+int aegkv_load_slices(int64_t num_slices, void* const* dst, const void* const* src,
+                      const int64_t* bytes, int mode, hipStream_t stream);
+
+/*
  * Transfer entries of many block tables in one call (host-only; no GPU).
  * Native form of BlockTable.transfer_entries (aegaeon/block_manager.py:
  * 446-478) over CacheGroupConfig.num_skipped_blocks / kernel_block_extent

@@ -651,6 +651,74 @@ def test_staged_swap_out_and_in_at_once(gpu, restore_tuning, dma_streams):
     pool.free()
 
 
+# ------------------------------------------------------------ weight loads --
+
+@pytest.mark.parametrize("mode,aligned", [("direct", True), ("direct", False),
+                                          ("staged", True), ("staged", False)])
+def test_load_slices_vs_expectation(gpu, mode, aligned):
+    """Weight slices of random sizes (empty, small, a few MiB) at random
+    offsets of one pinned pool and one device arena land byte for byte;
+    arena bytes outside the slices keep their guard value. Aligned: every
+    size and offset a 16 B multiple (the kernel's 16 B path); otherwise odd
+    sizes and offsets (its byte path)."""
+    rng = np.random.default_rng(31 + 2 * (mode == "staged") + aligned)
+    sizes = [0, 1, 15, 16, 4096, 8192 + 48, 3 << 20, 65537, 16 * 1000] + \
+        [int(x) for x in rng.integers(1, 200_000, 24)]
+    if aligned:
+        sizes = [-(-n // 16) * 16 for n in sizes]
+    host = ops.PinnedHostPool(64 << 20)
+    host.tensor.copy_(torch.from_numpy(rng.integers(0, 256, 64 << 20, dtype=np.uint8)))
+    arena = torch.full((64 << 20,), 0xA5, dtype=torch.uint8, device=gpu)
+    src, dst, hoff, doff = [], [], 0, 0
+    for n in sizes:
+        if not aligned:
+            hoff += int(rng.integers(0, 7))
+            doff += int(rng.integers(0, 7))
+        src.append(host.tensor.narrow(0, hoff, n))
+        dst.append(arena.narrow(0, doff, n))
+        hoff += -(-max(n, 1) // 256) * 256
+        doff += -(-max(n, 1) // 256) * 256
+    ops.load_slices(dst, src, mode=mode)
+    torch.cuda.synchronize()
+    covered = torch.zeros(64 << 20, dtype=torch.bool, device=gpu)
+    for d, h in zip(dst, src):
+        assert torch.equal(d, h.to(gpu))
+        if d.numel():
+            covered[d.data_ptr() - arena.data_ptr():][:d.numel()] = True
+    assert bool((arena[~covered] == 0xA5).all())
+    with pytest.raises(ValueError, match="overlap"):
+        ops.load_slices([arena.narrow(0, 0, 512), arena.narrow(0, 256, 512)],
+                        [host.tensor.narrow(0, 0, 512)] * 2, mode=mode)
+    with pytest.raises(ValueError, match="pinned"):
+        ops.load_slices([arena.narrow(0, 0, 64)], [torch.zeros(64, dtype=torch.uint8)], mode=mode)
+    host.free()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_qwen25_7b_weight_load_full_size(gpu, mode):
+    """A whole Qwen2.5-7B bf16 model (30 contents, 15.2 GB) from pinned
+    host memory into a device arena in one call: every content equals the
+    bytes it came from."""
+    from aegaeon_amd import weights
+
+    sizes = weights.qwen2_content_bytes()
+    host = weights.HostWeights(sizes)
+    dev_w = weights.DeviceWeights(sizes, gpu)
+    g = torch.Generator(device=gpu).manual_seed(7)
+    origin = []
+    for h in host.slices:      # random contents, written to the host through the DMA
+        o = torch.randint(0, 256, (h.numel(),), dtype=torch.uint8, device=gpu, generator=g)
+        h.copy_(o)
+        origin.append(o)
+    torch.cuda.synchronize()
+    weights.load_model(dev_w, host, mode=mode)
+    torch.cuda.synchronize()
+    for i, (d, o) in enumerate(zip(dev_w.slices, origin)):
+        assert torch.equal(d, o), i
+    del origin
+    host.free()
+
+
 # ------------------------------------------------------- uncached host pool --
 
 @pytest.mark.parametrize("mode", MODES)

@@ -598,6 +598,42 @@ def test_copy_probe_rejections_before_any_hip_call(aegkv_lib):
     assert call(_lib.PROBE_READ, src=np.array([], np.int64), dst=np.array([], np.int64)) == 0
 
 
+def test_load_slices_rejections_before_any_hip_call(aegkv_lib):
+    import numpy as np
+
+    from aegaeon_amd import _lib
+
+    P64 = ctypes.POINTER(ctypes.c_int64)
+
+    def call(dst, src, sizes, mode=1):
+        n = len(sizes)
+        d = (ctypes.c_void_p * max(n, 1))(*dst)
+        s_ = (ctypes.c_void_p * max(n, 1))(*src)
+        b = np.array(sizes, np.int64)
+        return aegkv_lib.aegkv_load_slices(n, d, s_, b.ctypes.data_as(P64), mode, None)
+
+    assert call([], [], []) == 0
+    assert call([0x10000], [0x20000], [0]) == 0                       # empty slices skipped
+    assert call([0x10000], [0x20000], [-1]) == _lib.EINVAL
+    assert call([0x10000], [0x20000], [16], mode=7) == _lib.EINVAL
+    assert call([0x10000, 0x10100], [0x20000, 0x30000], [512, 16]) == _lib.EOVERLAP
+    assert b"overlap" in aegkv_lib.aegkv_last_error()
+    assert call([0, 0x10000], [0x20000, 0x30000], [16, 16]) == _lib.EINVAL  # null target
+    assert aegkv_lib.aegkv_load_slices(2, None, None, None, 1, None) == _lib.EINVAL
+
+
+def test_qwen2_weight_contents():
+    """Qwen2.5-7B's contents add up to its 7.6 B bf16 parameters: the
+    embedding, 28 layers and the output head."""
+    from aegaeon_amd import weights
+
+    sizes = weights.qwen2_content_bytes()
+    assert len(sizes) == 30
+    params = sum(sizes) // 2
+    assert 7.60e9 < params < 7.63e9
+    assert sizes[1] == sizes[28] and sizes[0] == 152064 * 3584 * 2
+
+
 def test_copy_blocks_noalloc_limits(aegkv_lib):
     """Calls beyond the fixed descriptor array are refused with a clear
     error before anything else happens."""
