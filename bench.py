@@ -29,6 +29,7 @@ scatter them to 256 other ids.
 from __future__ import annotations
 
 import argparse
+import faulthandler
 import json
 import os
 import statistics
@@ -1032,6 +1033,8 @@ def bench_refplan(args):
 
 
 def main():
+    # a crash in native code prints the Python stack of every thread
+    faulthandler.enable()
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported here "

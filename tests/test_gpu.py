@@ -51,6 +51,36 @@ def test_legacy_swap_golden(gpu, golden, mode):
     assert np.array_equal(got, z["cache_after_in"])
 
 
+@pytest.mark.parametrize("dtype", [torch.uint8, torch.float32])
+def test_legacy_swap_block_size_for_other_dtypes(gpu, oracle, dtype):
+    """The one deliberate difference of ops.swap from swap.cu: the block is
+    kv_cache.numel() * element_size / size(0) bytes, where swap.cu:34 uses
+    numel * 2 / size(0) whatever the dtype. For bf16/fp16 the two agree
+    (test_legacy_swap_golden); for a 1-byte cache the reference's formula
+    gives twice the block (it would copy the next block too, and read past
+    the cache for the last one), for a 4-byte cache half of it. The product
+    moves exactly one block; the oracle, which keeps the reference's
+    formula, moves the other amount."""
+    n_dev, n_host, per_block = 8, 6, 64
+    elem = torch.tensor([], dtype=dtype).element_size()
+    rng = np.random.default_rng(elem)
+    cache_np = rng.integers(0, 256, n_dev * per_block * elem, dtype=np.uint8)
+    cache = torch.from_numpy(cache_np.copy()).view(dtype).view(n_dev, per_block).to(gpu)
+    pool = torch.zeros(n_host, per_block, dtype=dtype).pin_memory()
+    ops.swap([3], [1], False, cache, pool)
+    torch.cuda.synchronize()
+    block = per_block * elem
+    got = pool.view(torch.uint8).reshape(-1).numpy()
+    want = np.zeros(n_host * block, np.uint8)
+    want[block:2 * block] = cache_np[3 * block:4 * block]      # exactly one block
+    assert np.array_equal(got, want)
+    ref = np.zeros(n_host * block, np.uint8)
+    oracle.swap_legacy([3], [1], False, cache_np.copy(), cache_np.size // elem, n_dev, ref)
+    ref_block = (cache_np.size // elem) * 2 // n_dev            # swap.cu:34
+    assert ref_block == 2 * block // elem and ref_block != block
+    assert not np.array_equal(ref, want)                        # the documented difference
+
+
 @pytest.mark.parametrize("mode", MODES)
 def test_composite_swap_golden(gpu, golden, mode):
     z = golden("composite_swap.npz")
