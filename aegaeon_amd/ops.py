@@ -663,6 +663,10 @@ class HostFenceWords:
             self.owner = True
         else:
             name = _name
+            # a publish writes through the mapping: only this library's own files
+            if (os.path.dirname(os.path.abspath(name)) != "/dev/shm"
+                    or not os.path.basename(name).startswith("aegkv-fence-")):
+                raise ValueError(f"{name} is not a host fence file (/dev/shm/aegkv-fence-*)")
             fd = os.open(name, os.O_RDWR)
             self.owner = False
         try:

@@ -1251,7 +1251,9 @@ def _pinned_pool_scaled(page, n_out, n_in, scales=(1.0, 0.875, 0.75, 0.625, 0.5)
 
     gc.collect()
     torch.cuda.synchronize()
-    torch._C._host_emptyCache()
+    empty_host_cache = getattr(torch._C, "_host_emptyCache", None)   # torch's pinned cache
+    if empty_host_cache is not None:
+        empty_host_cache()
     _say("torch host cache after release:",
          {k: v for k, v in torch.cuda.host_memory_stats().items() if "current" in k})
     for scale in scales:

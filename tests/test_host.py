@@ -388,6 +388,8 @@ def test_host_fence_words_across_processes(aegkv_lib):
     assert ops.fence_host_wait(hw, 1, 6) and not ops.fence_host_wait(hw, 1, 8, 0.02)
     with pytest.raises(ValueError):
         hw.ptr(3)
+    with pytest.raises(ValueError, match="not a host fence file"):
+        ops.HostFenceWords.attach(str(REPO / "README.md"))
     name = hw.name
     hw.close()
     assert not os.path.exists(name)
