@@ -194,9 +194,11 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
  * ends, and is copied there with hipMemcpyAsync from a fixed (pageable) host
  * array, which the runtime has read when the call returns. Limits: at most
  * 1024 segments and 65536 pairs per call (AEGKV_ENOMEM beyond, nothing
- * enqueued). Every call on a device shares that device's array: calls that
- * overlap on one device (from other streams or threads) race and must be
- * ordered by the caller; calls on one stream are ordered by the stream.
+ * enqueued). Every call on a device shares that device's array, which keeps
+ * the last call's descriptor; nothing in it has to start at zero, since each
+ * call writes the whole descriptor it reads. Calls that overlap on one
+ * device (from other streams or threads) race and must be ordered by the
+ * caller; calls on one stream are ordered by the stream.
  */
 int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
                               const int64_t* segment_page_bytes, int64_t device_num_blocks,
