@@ -369,7 +369,12 @@ int aegkv_host_free(void* ptr);
  * gives up after `timeout_us` microseconds (0 < timeout_us <= 600 s) of
  * polling; it then stores 1 into *timed_out and lets the stream continue, so
  * the caller must check *timed_out (it is never cleared by the library)
- * before trusting what the stream produced after the wait.
+ * before trusting what the stream produced after the wait. A waiting fence
+ * holds its stream's hardware queue: the signal it waits for must come from
+ * another process or from a stream on a hardware queue of its own
+ * (aegkv_stream_create), never from a stream that may share the waiting
+ * stream's queue (plain streams share the process's few queues), or it
+ * runs only after the wait has timed out.
  */
 int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream);
 int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,

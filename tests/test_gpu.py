@@ -1918,3 +1918,107 @@ def test_tensor_parallel_ranks_share_host_pages(gpu):
             tv, t0v = t.view(n_blocks, -1), t0.view(n_blocks, -1)
             assert torch.equal(tv[back], t0v[src]), r
     pool.free()
+
+
+# ------------------------------------------- randomized weight-load cases --
+
+@pytest.mark.parametrize("case", range(24))
+def test_randomized_weight_loads(gpu, case):
+    """Random weight-load calls: 1-40 slices of 0 B-2 MiB at random 1 B or
+    16 B aligned offsets, random modes and stream kinds; every slice lands
+    byte for byte and the arena outside the slices keeps its guard value."""
+    rng = np.random.default_rng(7000 + case)
+    aligned = bool(rng.integers(0, 2))
+    mode = ("direct", "staged", "auto")[case % 3]
+    n = int(rng.integers(1, 41))
+    sizes = [int(rng.choice([0, 1, 16, 4096, int(rng.integers(1, 1 << 21))])) for _ in range(n)]
+    if aligned:
+        sizes = [-(-x // 16) * 16 for x in sizes]
+    total = sum(-(-max(x, 1) // 256) * 256 + 256 for x in sizes)
+    host = ops.PinnedHostPool(total)
+    host.tensor.copy_(torch.from_numpy(rng.integers(0, 256, total, dtype=np.uint8)))
+    arena = torch.full((total,), 0x3C, dtype=torch.uint8, device=gpu)
+    order = rng.permutation(n)                  # targets in another order than sources
+    src, dst, hoff = [], [None] * n, 0
+    doffs = np.zeros(n, np.int64)
+    off = 0
+    for k in order:
+        off += 0 if aligned else int(rng.integers(0, 16))
+        doffs[k] = off
+        off += -(-max(sizes[k], 1) // 256) * 256
+    for k in range(n):
+        hoff += 0 if aligned else int(rng.integers(0, 16))
+        src.append(host.tensor.narrow(0, hoff, sizes[k]))
+        dst[k] = arena.narrow(0, int(doffs[k]), sizes[k])
+        hoff += -(-max(sizes[k], 1) // 256) * 256
+    stream = torch.cuda.Stream(gpu) if case % 2 else None
+    _say("randomized weight load", case, mode, "aligned" if aligned else "bytes", n, "slices")
+    ops.load_slices(dst, src, mode=mode, stream=stream)
+    torch.cuda.synchronize()
+    covered = torch.zeros(total, dtype=torch.bool, device=gpu)
+    for d, h in zip(dst, src):
+        assert torch.equal(d, h.to(gpu))
+        if d.numel():
+            covered[d.data_ptr() - arena.data_ptr():][:d.numel()] = True
+    assert bool((arena[~covered] == 0x3C).all())
+    host.free()
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_randomized_noalloc_copies_vs_oracle(gpu, oracle, case):
+    """The allocation-free copy on random layouts (1-30 segments of random
+    16 B-multiple or odd pages, 2-3 calls in a row with shrinking and
+    growing pair lists) against the oracle's in-order copy."""
+    rng = np.random.default_rng(8000 + case)
+    n_seg = int(rng.integers(1, 31))
+    n_blocks = int(rng.integers(4, 97))
+    odd = rng.random() < 0.3
+    page = [int(rng.choice([16, 64, 4096, 16384, 48 * 1024])) + (int(rng.integers(1, 16)) if odd else 0)
+            for _ in range(n_seg)]
+    segs_np = [rng.integers(0, 256, (n_blocks, p), dtype=np.uint8) for p in page]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    calls = int(rng.integers(2, 4))
+    for _ in range(calls):
+        k = int(rng.integers(0, n_blocks // 2 + 1))
+        perm = rng.permutation(n_blocks)
+        src, dst = perm[:k], perm[k:2 * k]
+        ops.copy_blocks_noalloc(segs, src, dst)
+        oracle.copy_blocks([x.reshape(-1) for x in segs_np], np.array(page, np.int64), n_blocks,
+                           src, dst)
+    torch.cuda.synchronize()
+    for i in range(n_seg):
+        assert np.array_equal(segs[i].cpu().numpy(), segs_np[i]), i
+
+
+def test_fence_publish_from_several_streams_keeps_the_largest(gpu):
+    """Publishes of increasing counts from several streams into one host
+    word, each stream gated by its own device fence that the test releases
+    in reverse order: the word ends at the largest count, never goes down,
+    and each stream's count shows up only after its gate opened. Every
+    stream has a hardware queue of its own: a waiting fence holds its queue,
+    so a signal queued behind it on a shared queue would wait for the
+    wait's time-out."""
+    words = torch.zeros(4, dtype=torch.int64, device=gpu)
+    flags = torch.zeros(4, dtype=torch.int64, device=gpu)
+    hw = ops.HostFenceWords(1)
+    owners = [ops.DedicatedStream(gpu) for _ in range(5)]
+    try:
+        streams = [o.stream for o in owners[:4]]
+        torch.cuda.synchronize()
+        for i, st in enumerate(streams):
+            ops.fence_wait(words, i, 1, flags, i, timeout_s=60, stream=st)
+            ops.fence_publish(hw, 0, 10 * (i + 1), device=gpu, stream=st)
+        assert not ops.fence_host_wait(hw, 0, 1, timeout_s=0.1)
+        releaser = owners[4].stream
+        seen = []
+        for i in reversed(range(4)):
+            ops.fence_signal(words, i, 1, stream=releaser)
+            streams[i].synchronize()
+            seen.append(int(hw.words[0]))
+        assert seen == [40, 40, 40, 40]          # the largest count came first and stays
+        assert int(flags.sum()) == 0
+    finally:
+        torch.cuda.synchronize()
+        for o in owners:
+            o.close()
+        hw.close()
