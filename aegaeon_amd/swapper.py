@@ -81,6 +81,13 @@ class FenceToken:
 
 _ipc_event_refusal: Dict[int, Optional[str]] = {}
 
+# Fences raised by swappers of this process: (address of the fence word,
+# slot) -> (count, completion event of the swap that raised it). A waiting
+# fence kernel holds its stream's hardware queue, and a stream of this
+# process may share that queue with the producing stream, so a token
+# produced here is waited on through the producer's event instead.
+_local_fences: Dict[Tuple[int, int], Tuple[int, torch.cuda.Event]] = {}
+
 
 def interprocess_event_refusal(device: torch.device) -> Optional[str]:
     """None if this process's HIP runtime records interprocess events on
@@ -292,6 +299,12 @@ class KVSwapper:
                 if isinstance(ev, FenceToken):
                     if self.fence_words is None:
                         raise ValueError("a FenceToken source needs fence_words")
+                    local = _local_fences.get((self.fence_words.data_ptr(), ev.slot))
+                    if local is not None and local[0] >= ev.value:
+                        # raised in this process: the swap of count local[0]
+                        # follows the one the token names on its stream
+                        stream.wait_event(local[1])
+                        continue
                     ops.fence_wait(self.fence_words, ev.slot, ev.value, self._fence_timed_out,
                                    side, timeout_s=self.fence_timeout_s, stream=stream)
                 else:
@@ -306,13 +319,14 @@ class KVSwapper:
         new_event.record(stream)
         for rid in request_ids:
             self.move_event_table[rid].append(new_event)
-        self._signal(side, stream)
+        self._signal(side, stream, new_event)
 
-    def _signal(self, side: int, stream) -> None:
+    def _signal(self, side: int, stream, event: torch.cuda.Event) -> None:
         if self.fence_slots is not None:
             self._fence_count[side] += 1
             slot, count = self.fence_slots[side], self._fence_count[side]
             ops.fence_signal(self.fence_words, slot, count, stream=stream)
+            _local_fences[(self.fence_words.data_ptr(), slot)] = (count, event)
             host = None
             if self.fence_host is not None:
                 ops.fence_publish(self.fence_host, slot, count, device=self.device,

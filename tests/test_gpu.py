@@ -1688,6 +1688,47 @@ def test_fence_wait_gives_up_after_its_budget(gpu):
     pool.free()
 
 
+def test_same_process_fence_token_waits_on_the_producers_event(gpu):
+    """A FenceToken raised by a swapper of this process, handed to another
+    swapper of this process as a source event, orders the consumer through
+    the producer's completion event: the consumer's swap-in reads the host
+    pages the producer's swap-out wrote, with no fence wait to time out
+    (a waiting fence would hold its queue, which plain streams of one
+    process may share with the producer's)."""
+    import time
+
+    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
+    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
+    from aegaeon_amd.swapper import FenceToken, KVSwapper, _local_fences
+
+    n_blocks, page = 64, 256 * 1024
+    caches = [allocate_composite_cache([KVCacheTensorSpec(n_blocks * page, ("l0",))], n_blocks,
+                                       gpu) for _ in range(2)]
+    caches[0].backing[0].random_(-128, 127)
+    words = torch.zeros(8, dtype=torch.int64, device=gpu)
+    pool = ops.PinnedHostPool(32 * page)
+    descr = [CacheGroupRuntimeConfig("attention", 16, 16)]
+    a = KVSwapper(caches[0], [{"l0"}], descr, pool.tensor, fence_words=words, fence_slots=(0, 1),
+                  fence_timeout_s=30)
+    b = KVSwapper(caches[1], [{"l0"}], descr, pool.tensor, fence_words=words, fence_slots=(2, 3),
+                  fence_timeout_s=30)
+    torch.cuda.synchronize()
+    src, host, dst = list(range(1, 31)), list(range(30)), list(range(33, 63))
+    t0 = time.perf_counter()
+    a.swap_blocks([1], src, host, [0] * 30, [0] * 30, [1] * 30, [None], False)
+    token = a.last_fence
+    assert token == FenceToken(0, 1)
+    assert _local_fences[(words.data_ptr(), 0)][0] == 1
+    b.swap_blocks([1], host, dst, [0] * 30, [0] * 30, [1] * 30, [token], True)
+    b.wait_for_all_move_in()               # raises if a fence wait had timed out
+    assert time.perf_counter() - t0 < 10
+    si, di = torch.tensor(src, device=gpu), torch.tensor(dst, device=gpu)
+    assert torch.equal(caches[1].segment_pages(0)[di], caches[0].segment_pages(0)[si])
+    a.close()
+    b.close()
+    pool.free()
+
+
 def _fence_producer(q_in, q_out):
     """Child process: open the parent's fence words and cache blocks, then,
     when told, write a pattern late and signal the fence behind it."""
