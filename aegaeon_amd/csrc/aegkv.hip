@@ -193,6 +193,7 @@ struct CopySeg {            // one backing tensor of a block copy
   int64_t pad;
 };
 static_assert(sizeof(CopySeg) == 32, "CopySeg layout");
+static_assert(sizeof(PairDesc) == 16, "PairDesc layout (descriptors are whole 16-byte words)");
 
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) v4u gv4u;  // global (VM) address space
@@ -410,6 +411,24 @@ __global__ __launch_bounds__(WG) void slices_kernel(const SliceDesc* __restrict_
     else
       move_chunk_bytes<WG>(sl.src + begin, sl.dst + begin, nbytes);
   }
+}
+
+// Descriptor bytes carried in one launch's kernel arguments (allocation-free
+// copies): lane i stores the i-th 16 bytes. The runtime copies a launch's
+// arguments when the launch is enqueued, and a graph that captures the
+// launch keeps its own copy, so the host buffer they came from is free as
+// soon as the launch call returns.
+constexpr uint32_t kFillBytes = 2048;
+struct FillArgs {
+  v4u data[kFillBytes / 16];
+  v4u* dst;
+  uint32_t words;  // 16-byte words to store, <= kFillBytes / 16
+  uint32_t pad;
+};
+
+__global__ __launch_bounds__(kFillBytes / 16) void desc_fill_kernel(FillArgs a) {
+  const uint32_t i = threadIdx.x;
+  if (i < a.words) a.dst[i] = a.data[i];
 }
 
 // Shapes the library instantiates. 1024-lane shapes move 16 KiB rows; a
@@ -1548,11 +1567,13 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
 // aegkv_copy_blocks_noalloc: aegkv_copy_blocks for callers that cannot
 // allocate. The descriptor (segment table + pair table) goes to `scratch`,
 // a fixed device array every GPU holds for the life of the process, instead
-// of the library's upload ring; the ids are checked with fixed host arrays
-// instead of a block-indexed map. Nothing is allocated on the host or the
-// device. Every call on a device shares that device's array, so calls that
-// overlap on one device (different streams, or threads) race; calls on one
-// stream are ordered.
+// of the library's upload ring; it travels in the kernel arguments of small
+// fill launches (2 KiB each), so a graph that captures the call replays its
+// own descriptor. The ids are checked with fixed host arrays instead of a
+// block-indexed map. Nothing is allocated on the host or the device. Every
+// call on a device shares that device's array, so calls that overlap on one
+// device (different streams, or threads, or a graph replayed beside other
+// calls) race; calls on one stream are ordered.
 
 constexpr int32_t kNoAllocMaxSegments = 1024;
 constexpr int64_t kNoAllocMaxPairs = 65536;
@@ -1585,6 +1606,24 @@ int noalloc_scratch(int dev, char** out, int* num_cus) {
   *out = g_scratch_ptr[dev];
   *num_cus = g_noalloc_cus[dev];
   return 0;
+}
+
+// dst[0, bytes) <- src[0, bytes) on `stream`, kFillBytes per launch of
+// desc_fill_kernel (bytes is a multiple of 16; descriptors are).
+hipError_t noalloc_fill(char* dst, const unsigned char* src, size_t bytes, hipStream_t stream) {
+  FillArgs a;
+  a.pad = 0;
+  for (size_t off = 0; off < bytes; off += kFillBytes) {
+    const size_t n = std::min<size_t>(kFillBytes, bytes - off);
+    std::memcpy(a.data, src + off, n);
+    a.dst = reinterpret_cast<v4u*>(dst + off);
+    a.words = static_cast<uint32_t>(n / 16);
+    (void)hipGetLastError();  // clear a stale error: the check below is for this launch
+    hipLaunchKernelGGL(desc_fill_kernel, dim3(1), dim3(kFillBytes / 16), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 int copy_noalloc(int32_t num_segments, void* const* bases, const int64_t* page_bytes,
@@ -1622,10 +1661,12 @@ int copy_noalloc(int32_t num_segments, void* const* bases, const int64_t* page_b
   pack_copy_desc(reinterpret_cast<char*>(g_noalloc_host), num_segments, bases, bases,
                  page_bytes, num_pairs, src_ids, dst_ids);
   const size_t total = copy_pair_offset(num_segments) + sizeof(PairDesc) * num_pairs;
-  // From pageable memory the runtime has taken the bytes when the call
-  // returns, so the packing area is free for the next call.
-  AEGKV_HIP(hipMemcpyAsync(dv, g_noalloc_host, total, hipMemcpyHostToDevice, stream));
-  hipError_t e = copy_launch(plan, t, num_cus, num_segments, dv, stream);
+  // The descriptor reaches `scratch` through kernel arguments, not a copy
+  // from the packing area: a copy node captured into a graph would read the
+  // packing area again at every replay, after later calls rewrote it.
+  hipError_t e = noalloc_fill(dv, g_noalloc_host, total, stream);
+  if (e != hipSuccess) return hip_fail(e, "desc_fill_kernel launch");
+  e = copy_launch(plan, t, num_cus, num_segments, dv, stream);
   if (e != hipSuccess) return hip_fail(e, "copy_blocks_kernel launch");
   return 0;
 }

@@ -191,14 +191,17 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
  * loops, harnesses that forbid hipMalloc). The call allocates nothing on
  * the host or the device: the descriptor goes to a fixed device array of
  * 1,081,344 bytes that each GPU the library runs on holds until the process
- * ends, and is copied there with hipMemcpyAsync from a fixed (pageable) host
- * array, which the runtime has read when the call returns. Limits: at most
- * 1024 segments and 65536 pairs per call (AEGKV_ENOMEM beyond, nothing
+ * ends, written there by small fill kernels whose arguments carry the
+ * descriptor (2 KiB per launch; 4096 pairs over 80 segments take 34
+ * launches). A graph that captures the call therefore replays the
+ * descriptor it captured, whatever calls ran since. Limits: at most 1024
+ * segments and 65536 pairs per call (AEGKV_ENOMEM beyond, nothing
  * enqueued). Every call on a device shares that device's array, which keeps
  * the last call's descriptor; nothing in it has to start at zero, since each
  * call writes the whole descriptor it reads. Calls that overlap on one
- * device (from other streams or threads) race and must be ordered by the
- * caller; calls on one stream are ordered by the stream.
+ * device (from other streams or threads, or a graph replayed beside other
+ * calls) race and must be ordered by the caller; calls on one stream are
+ * ordered by the stream.
  */
 int aegkv_copy_blocks_noalloc(int32_t num_segments, void* const* segment_bases,
                               const int64_t* segment_page_bytes, int64_t device_num_blocks,

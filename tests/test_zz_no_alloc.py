@@ -86,3 +86,44 @@ def test_copy_blocks_noalloc_after_rejection_and_on_a_second_stream(gpu):
     for x, y in zip(a, b):
         assert torch.equal(x, y)
     assert ctypes.sizeof(ctypes.c_int64) == 8 and _lib.load().aegkv_copy_blocks_noalloc
+
+
+def test_copy_blocks_noalloc_under_graph_capture(gpu):
+    """A graph that captures the call replays its own descriptor. Between
+    replays the test rewrites the captured targets and makes other
+    allocation-free calls (which rewrite the library's packing area and the
+    device array), then synchronizes; each of three replays must copy the
+    captured pairs, and only those. The captured descriptor (250 pairs over
+    12 segments, 4512 bytes) spans three fill launches."""
+    _say("copy_blocks_noalloc under graph capture")
+    rng = np.random.default_rng(11)
+    n_seg, n_blocks, page = 12, 1024, 32 * 1024
+    a, _ = _caches(n_seg, n_blocks, page, 11, gpu)
+    perm = rng.permutation(n_blocks)
+    sa, da = perm[:250], perm[250:500]          # captured pairs
+    sb, db = perm[500:600], perm[600:700]       # eager pairs between replays
+    ops.copy_blocks_noalloc(a, sb[:1], db[:1])  # first call on the device outside the capture
+    torch.cuda.synchronize()
+    before = [t.clone() for t in a]
+    graph = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream(gpu)
+    with torch.cuda.graph(graph, stream=st):
+        ops.copy_blocks_noalloc(a, sa, da)
+    torch.cuda.synchronize()
+    for x, y in zip(a, before):
+        assert torch.equal(x, y)  # capturing ran nothing
+    ia, ja = torch.from_numpy(sa).to(gpu), torch.from_numpy(da).to(gpu)
+    for r in range(3):
+        for t in a:
+            t[ja] = r + 1
+        k = 30 * r
+        ops.copy_blocks_noalloc(a, sb[k:k + 30], db[k:k + 30])
+        torch.cuda.synchronize()
+        want = [t.clone() for t in a]
+        for w in want:
+            w[ja] = w[ia]
+        graph.replay()
+        torch.cuda.synchronize()
+        for i in range(n_seg):
+            assert torch.equal(a[i], want[i]), (r, i)
+    del graph
