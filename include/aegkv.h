@@ -21,9 +21,10 @@
  *     calling thread's most recent failure.
  *   - The caller keeps every buffer alive until the stream has passed the
  *     enqueued work (record an event after the call and wait on it).
- *   - Calls are not for stream capture (hipGraph): their descriptors are
- *     uploaded from a host ring at enqueue time, which a graph replay would
- *     not repeat.
+ *   - Calls are not for stream capture (hipGraph), except
+ *     aegkv_copy_blocks_noalloc: their descriptors are copied from a host
+ *     ring whose slots later calls reuse, and a replayed copy would read
+ *     whatever the slot holds then.
  */
 #ifndef AEGKV_H
 #define AEGKV_H
