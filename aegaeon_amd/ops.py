@@ -465,10 +465,11 @@ class _OwnedStream(torch.cuda.ExternalStream):
         if ptr:
             _lib.load().aegkv_stream_destroy(ctypes.c_void_p(ptr))
 
-    def __del__(self):
+    def __del__(self, _finalizing=sys.is_finalizing):
         # At interpreter exit the HIP runtime may already be torn down, and
-        # the process is ending anyway: leave the stream to it.
-        if sys.is_finalizing():
+        # the process is ending anyway: leave the stream to it. (The check is
+        # bound at definition: module globals may be gone by then.)
+        if _finalizing():
             return
         try:
             self._aegkv_close()
