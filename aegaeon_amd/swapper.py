@@ -29,6 +29,7 @@ Ray object refs are not part of this module.
 from __future__ import annotations
 
 import logging
+import weakref
 from collections import defaultdict
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple, Union
@@ -81,12 +82,32 @@ class FenceToken:
 
 _ipc_event_refusal: Dict[int, Optional[str]] = {}
 
-# Fences raised by swappers of this process: (address of the fence word,
-# slot) -> (count, completion event of the swap that raised it). A waiting
-# fence kernel holds its stream's hardware queue, and a stream of this
-# process may share that queue with the producing stream, so a token
-# produced here is waited on through the producer's event instead.
-_local_fences: Dict[Tuple[int, int], Tuple[int, torch.cuda.Event]] = {}
+# Fences raised by swappers of this process: (address of the fence words,
+# slot) -> (count, completion event of the swap that raised it, the raising
+# swapper). A waiting fence kernel holds its stream's hardware queue, and a
+# stream of this process may share that queue with the producing stream, so
+# a token produced here is waited on through the producer's event instead.
+# An entry holds only while its swapper lives: the swapper keeps its fence
+# words alive, and once both are gone the address may belong to other words.
+_local_fences: Dict[Tuple[int, int], Tuple[int, torch.cuda.Event, "weakref.ref"]] = {}
+
+
+def _note_local_fence(words_ptr: int, slot: int, count: int, event, owner) -> None:
+    _local_fences[(words_ptr, slot)] = (count, event, weakref.ref(owner))
+
+
+def _local_fence_event(words_ptr: int, slot: int, value: int):
+    """The event of this process's swap that raised (words, slot) to at
+    least `value`, or None (not raised here, not that far yet, or raised by
+    a swapper that no longer exists)."""
+    entry = _local_fences.get((words_ptr, slot))
+    if entry is None:
+        return None
+    count, event, owner = entry
+    if owner() is None:
+        del _local_fences[(words_ptr, slot)]
+        return None
+    return event if count >= value else None
 
 
 def interprocess_event_refusal(device: torch.device) -> Optional[str]:
@@ -299,11 +320,11 @@ class KVSwapper:
                 if isinstance(ev, FenceToken):
                     if self.fence_words is None:
                         raise ValueError("a FenceToken source needs fence_words")
-                    local = _local_fences.get((self.fence_words.data_ptr(), ev.slot))
-                    if local is not None and local[0] >= ev.value:
-                        # raised in this process: the swap of count local[0]
-                        # follows the one the token names on its stream
-                        stream.wait_event(local[1])
+                    local = _local_fence_event(self.fence_words.data_ptr(), ev.slot, ev.value)
+                    if local is not None:
+                        # raised in this process: the swap that raised it this
+                        # far follows the one the token names on its stream
+                        stream.wait_event(local)
                         continue
                     ops.fence_wait(self.fence_words, ev.slot, ev.value, self._fence_timed_out,
                                    side, timeout_s=self.fence_timeout_s, stream=stream)
@@ -326,7 +347,7 @@ class KVSwapper:
             self._fence_count[side] += 1
             slot, count = self.fence_slots[side], self._fence_count[side]
             ops.fence_signal(self.fence_words, slot, count, stream=stream)
-            _local_fences[(self.fence_words.data_ptr(), slot)] = (count, event)
+            _note_local_fence(self.fence_words.data_ptr(), slot, count, event, self)
             host = None
             if self.fence_host is not None:
                 ops.fence_publish(self.fence_host, slot, count, device=self.device,

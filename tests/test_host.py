@@ -414,6 +414,32 @@ def test_host_fence_rejections_before_any_hip_call(aegkv_lib):
     assert lib.aegkv_fence_host_wait(base, 6, 1000) == 0
 
 
+def test_local_fence_entries_end_with_their_swapper():
+    """A fence token raised in this process is waited on through the
+    raising swap's event only while the raising swapper exists: once it is
+    gone, its fence words may have been freed and the address reused by
+    other words, so the entry must not answer for them."""
+    import gc
+
+    from aegaeon_amd import swapper as swm
+
+    class Raiser:
+        pass
+
+    raiser, ev = Raiser(), object()
+    addr = 0x7F00_0000_1000
+    swm._note_local_fence(addr, 3, 5, ev, raiser)
+    assert swm._local_fence_event(addr, 3, 5) is ev
+    assert swm._local_fence_event(addr, 3, 2) is ev      # later raise covers earlier counts
+    assert swm._local_fence_event(addr, 3, 6) is None    # not raised that far yet
+    assert swm._local_fence_event(addr, 4, 1) is None    # another slot
+    assert swm._local_fence_event(addr + 8, 3, 1) is None
+    del raiser
+    gc.collect()
+    assert swm._local_fence_event(addr, 3, 1) is None
+    assert (addr, 3) not in swm._local_fences
+
+
 def test_tuning_knobs(aegkv_lib):
     from aegaeon_amd import _lib
 
