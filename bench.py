@@ -71,6 +71,9 @@ def parse():
                    help="switch config: KV swaps only, no weight loads")
     p.add_argument("--no-cu-partition", action="store_true",
                    help="overlap config: run the three streams on every CU")
+    p.add_argument("--no-copy-partition", action="store_true",
+                   help="skip the copy_blocks run on a 24-CU-per-XCD stream (keeps the "
+                        "copy kernel's launches to the roofline ones)")
     p.add_argument("--no-side-by-side", action="store_true",
                    help="skip the DIRECT vs STAGED side-by-side measurement")
     p.add_argument("--no-reference-loop", action="store_true",
@@ -1186,8 +1189,10 @@ def main():
     log("read-only and write-only probes over the copy's tiles")
     probes = copy_probes(torch, ops, segs2, csrc, cdst, copy_bytes // 2)
 
-    log("the same copy on a stream confined to 24 CUs of every XCD")
-    part = copy_on_cu_partition(torch, ops, segs2, csrc, cdst, copy_bytes, 24)
+    part = None
+    if not args.no_copy_partition:
+        log("the same copy on a stream confined to 24 CUs of every XCD")
+        part = copy_on_cu_partition(torch, ops, segs2, csrc, cdst, copy_bytes, 24)
 
     t_d2h, t_h2d, t_cpy = sum(d2h) / len(d2h), sum(h2d) / len(h2d), sum(cpy) / len(cpy)
     d2h_gbps = swap_bytes / t_d2h / 1e9
@@ -1262,7 +1267,7 @@ def main():
             "rw_bound_frac_hbm_peak": round(probes["rw_bound"] / HBM_PEAK_GBPS, 4),
             "copy_frac_of_rw_bound": round(copy_gbps / probes["rw_bound"], 4),
         },
-        "copy_blocks_cu_partition": dict(part, what=(
+        "copy_blocks_cu_partition": None if part is None else dict(part, what=(
             "the same copy on a dedicated stream masked to CUs 0-23 of every XCD "
             "(DedicatedStream(cu_mask=xcd_cu_mask(24))), a caller's choice, not the roofline "
             "value: one tile in flight per CU on 192 CUs instead of 256")),
