@@ -398,7 +398,8 @@ TILE_SHAPES = (   # (name, layers, blocks, kv_heads): tiles of 16 x heads x 128 
 
 def bench_tiles(args):
     """copy_blocks by tile size, beside its read-only and write-only probes
-    on the same tiles: each BASELINE KV shape, pairs = two disjoint seeded
+    on the same tiles: each workload's KV shape (Qwen2.5-7B, Qwen3-4B,
+    Qwen1.5-MoE, Llama-2-13B), pairs = two disjoint seeded
     halves of the blocks (every block is a source or a target)."""
     import numpy as np
     import torch
