@@ -534,6 +534,21 @@ int get_ctx(DeviceCtx** out) {
   return 0;
 }
 
+// Entry points that upload their descriptors through the host ring cannot
+// be captured into a graph: a replay would copy the descriptor from the
+// ring slot as a later call left it. They refuse a capturing stream before
+// anything is enqueued (aegkv_copy_blocks_noalloc is the capturable copy).
+int refuse_capture(hipStream_t stream) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(stream, &status);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (status != hipStreamCaptureStatusNone)
+    return fail(AEGKV_EINVAL, "the stream is being captured: this call uploads its descriptor "
+                "through a host ring that later calls reuse, so a graph replay would read "
+                "another call's descriptor (aegkv_copy_blocks_noalloc can be captured)");
+  return 0;
+}
+
 int ring_grow(Ring& r, size_t need) {
   // Retire everything, then replace the buffers.
   for (auto& reg : r.inflight) {
@@ -1297,6 +1312,8 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   if (E.n == 0) return 0;
   rc = check_layout_pointers(L);
   if (rc) return rc;
+  rc = refuse_capture(stream);
+  if (rc) return rc;
   DeviceCtx* ctx = nullptr;
   rc = get_ctx(&ctx);
   if (rc) return rc;
@@ -1538,6 +1555,8 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   CopyPlan plan;
   rc = copy_plan(t, vec, max_page, num_segments, num_pairs, &plan);
   if (rc) return rc;
+  rc = refuse_capture(stream);
+  if (rc) return rc;
   DeviceCtx* ctx = nullptr;
   rc = get_ctx(&ctx);
   if (rc) return rc;
@@ -1724,8 +1743,10 @@ int slices_core(int64_t n, void* const* dst, const void* const* src, const int64
   if (items >= (int64_t(1) << 32) || keep.size() >= (size_t(1) << 32))
     return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
                 static_cast<long long>(items));
+  int rc = refuse_capture(stream);
+  if (rc) return rc;
   DeviceCtx* ctx = nullptr;
-  int rc = get_ctx(&ctx);
+  rc = get_ctx(&ctx);
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(ctx->mu);
   const size_t total = sizeof(SliceDesc) * keep.size();

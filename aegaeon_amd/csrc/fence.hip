@@ -156,8 +156,15 @@ int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream)
   if (rc) return rc;
   if (value == 0 || value >= (uint64_t(1) << 63))
     return fail(AEGKV_EINVAL, "fence values are positive and below 2^63");
+  // The callback frees its record, so a graph replaying it would use a
+  // freed record: refuse a capturing stream.
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &status);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+  if (status != hipStreamCaptureStatusNone)
+    return fail(AEGKV_EINVAL, "fence publish cannot be captured into a graph");
   Publish* p = new Publish{host_word, value};
-  hipError_t e = hipLaunchHostFunc(stream, publish_cb, p);
+  e = hipLaunchHostFunc(stream, publish_cb, p);
   if (e != hipSuccess) {
     delete p;
     return hip_fail(e, "hipLaunchHostFunc(fence publish)");

@@ -24,7 +24,11 @@
  *   - Calls are not for stream capture (hipGraph), except
  *     aegkv_copy_blocks_noalloc: their descriptors are copied from a host
  *     ring whose slots later calls reuse, and a replayed copy would read
- *     whatever the slot holds then.
+ *     whatever the slot holds then. On a capturing stream they return
+ *     AEGKV_EINVAL with nothing enqueued (aegkv_load_slices in STAGED mode,
+ *     runtime copies from the pinned sources only, is capturable;
+ *     aegkv_fence_signal and aegkv_fence_wait take their arguments by value
+ *     and are too; aegkv_fence_publish refuses a capturing stream).
  */
 #ifndef AEGKV_H
 #define AEGKV_H

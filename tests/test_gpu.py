@@ -2063,3 +2063,75 @@ def test_fence_publish_from_several_streams_keeps_the_largest(gpu):
         for o in owners:
             o.close()
         hw.close()
+
+
+def _capture(gpu, fn):
+    """Run fn() under torch.cuda.graph capture on a side stream; returns
+    the graph (the caller replays it)."""
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream(gpu)
+    with torch.cuda.graph(g, stream=st):
+        fn()
+    return g
+
+
+def test_ring_entry_points_refuse_graph_capture(gpu):
+    """Calls that upload their descriptors through the library's host ring
+    (and the fence publish, whose host callback frees its record) return
+    AEGKV_EINVAL on a capturing stream with nothing enqueued, so a graph
+    can never replay a reused ring slot; the library works normally after."""
+    _say("ring entry points under graph capture")
+    a = [torch.randint(0, 256, (64, 4096), dtype=torch.uint8, device=gpu) for _ in range(3)]
+    kv = torch.randint(0, 256, (64, 4096), dtype=torch.uint8, device=gpu)
+    host = ops.PinnedHostPool(64 * 4096)
+    hw = ops.HostFenceWords(1)
+    dev_w = torch.zeros(1 << 16, dtype=torch.uint8, device=gpu)
+    host_w = ops.PinnedHostPool(1 << 16)
+    torch.cuda.synchronize()
+    calls = [
+        ("copy_blocks", lambda: ops.copy_blocks(a, [1, 2], [3, 4])),
+        ("swap", lambda: ops.swap([1, 5], [2, 6], False, kv, host.tensor)),
+        ("load_slices direct", lambda: ops.load_slices([dev_w], [host_w.tensor], mode="direct")),
+        ("fence_publish", lambda: ops.fence_publish(hw, 0, 1, device=gpu,
+                                                    stream=torch.cuda.current_stream(gpu))),
+    ]
+    for name, fn in calls:
+        with pytest.raises(ValueError, match="captured"):
+            _capture(gpu, fn)
+        torch.cuda.synchronize()
+    assert int(hw.words[0]) == 0
+    before = [t.clone() for t in a]
+    ops.copy_blocks(a, [1, 2], [3, 4])
+    torch.cuda.synchronize()
+    for t, b in zip(a, before):
+        assert torch.equal(t[[3, 4]], b[[1, 2]])
+    hw.close()
+    host.free()
+    host_w.free()
+
+
+def test_fence_signal_and_wait_replay_from_a_graph(gpu):
+    """The fence kernels take their arguments by value, so a captured signal
+    and wait replay as captured: three replays, the word reset eagerly
+    before each, each ending with the word at the captured value and no
+    time-out flagged."""
+    words = torch.zeros(2, dtype=torch.int64, device=gpu)
+    flags = torch.zeros(2, dtype=torch.int64, device=gpu)
+    torch.cuda.synchronize()
+
+    def body():
+        st = torch.cuda.current_stream(gpu)
+        ops.fence_signal(words, 1, 5, stream=st)
+        ops.fence_wait(words, 1, 5, flags, 1, timeout_s=10, stream=st)
+
+    g = _capture(gpu, body)
+    torch.cuda.synchronize()
+    assert int(words[1]) == 0          # capturing ran nothing
+    for r in range(3):
+        words.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(words[1]) == 5, r
+        assert int(flags.sum()) == 0, r
+    del g
