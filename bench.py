@@ -43,6 +43,9 @@ sys.path.insert(0, str(REPO))
 
 METRIC = ("KV swap GB/s (D2H/H2D, % host link) + HBM block-copy GB/s (% HBM peak)")
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
+# PCIe 5.0 x16, one direction: 16 lanes x 32 GT/s x 128/130 encoding; packet
+# headers take a further share, which the measured link rate includes
+PCIE_GEN5_X16_GBPS = round(16 * 32e9 * 128 / 130 / 8 / 1e9, 3)
 TRAFFIC_FILE = REPO / "profiles" / "copy_blocks_traffic.json"
 
 
@@ -1284,6 +1287,9 @@ def main():
             "frac_h2d": round(h2d_gbps / link["h2d"], 4),
             "avg_launch_ms_d2h": round(t_d2h * 1e3, 3),
             "avg_launch_ms_h2d": round(t_h2d * 1e3, 3),
+            "pcie_gen5_x16_GBps": PCIE_GEN5_X16_GBPS,
+            "frac_d2h_of_pcie": round(d2h_gbps / PCIE_GEN5_X16_GBPS, 4),
+            "frac_h2d_of_pcie": round(h2d_gbps / PCIE_GEN5_X16_GBPS, 4),
         },
     }
     line["overlap"] = overlap
