@@ -199,7 +199,10 @@ int aegkv_copy_blocks(int32_t num_segments, void* const* segment_bases,
  * ends, written there by small fill kernels whose arguments carry the
  * descriptor (2 KiB per launch; 4096 pairs over 80 segments take 34
  * launches). A graph that captures the call therefore replays the
- * descriptor it captured, whatever calls ran since. Limits: at most 1024
+ * descriptor it captured, whatever calls ran since. The launches cost host
+ * time: measured 0.48 ms per call for 4096 pairs over 80 segments and
+ * 7.0 ms for 65536 pairs, against 0.10-0.11 ms for aegkv_copy_blocks; the
+ * same for up to a few hundred pairs. Limits: at most 1024
  * segments and 65536 pairs per call (AEGKV_ENOMEM beyond, nothing
  * enqueued). Every call on a device shares that device's array, which keeps
  * the last call's descriptor; nothing in it has to start at zero, since each
