@@ -17,7 +17,7 @@ import torch  # noqa: F401  (must precede loading libaegkv, see module doc)
 
 LIB_PATH = Path(__file__).resolve().parent / "libaegkv.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 EINVAL = -1
@@ -48,12 +48,17 @@ TUNE_STAGED_OVERLAP = 14
 TUNE_SWAP_OUT_WORKGROUPS_UNCACHED = 15
 TUNE_COPY_LANES = 17
 HOST_UNCACHED = 1
+HOST_COHERENT = 2
 PROBE_READ = 1
 PROBE_WRITE = 2
+#: bit 62 of a fence word: the move behind it (or one before it on the same
+#: stream) failed
+FENCE_FAILED = 1 << 62
 
 #: every symbol include/aegkv.h declares
 EXPORTED_SYMBOLS = (
     "aegkv_abi_version",
+    "aegkv_init",
     "aegkv_last_error",
     "aegkv_tune",
     "aegkv_swap",
@@ -67,13 +72,16 @@ EXPORTED_SYMBOLS = (
     "aegkv_host_alloc",
     "aegkv_host_alloc_flags",
     "aegkv_host_free",
+    "aegkv_host_usage",
     "aegkv_fence_signal",
     "aegkv_fence_wait",
     "aegkv_fence_publish",
     "aegkv_fence_host_wait",
+    "aegkv_guard_merge",
     "aegkv_stream_create",
     "aegkv_stream_create_masked",
     "aegkv_stream_destroy",
+    "aegkv_stream_release",
 )
 
 _P = ctypes.c_void_p
@@ -87,19 +95,21 @@ _PP = ctypes.POINTER(ctypes.c_void_p)
 
 _SIGNATURES = {
     "aegkv_abi_version": (_INT, []),
+    "aegkv_init": (_INT, []),
     "aegkv_last_error": (ctypes.c_char_p, []),
     "aegkv_tune": (_I64, [_INT, _I64]),
     "aegkv_swap": (_INT, [_I64P, _I64P, _I64, _INT, _P, _I64, _P, _I64, _I64, _INT, _P]),
     "aegkv_swap_blocks": (
         _INT,
         [_I32, _PP, _I64P, _I64P, _U64P, _I64, _I32, _I64P, _P, _I64, _I64, _I64, _I64,
-         _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P],
+         _I64P, _I64P, _I32P, _I64P, _I64P, _INT, _INT, _P, _P],
     ),
     "aegkv_copy_blocks": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_copy_blocks_noalloc": (_INT, [_I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P]),
     "aegkv_copy_probe": (_INT, [_INT, _I32, _PP, _I64P, _I64, _I64, _I64P, _I64P, _P,
                                 ctypes.c_uint32, _P]),
-    "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P]),
+    "aegkv_migrate_blocks": (_INT, [_I32, _PP, _PP, _I64P, _I64, _I64, _I64, _I64P, _I64P, _P,
+                                    _P]),
     "aegkv_load_slices": (_INT, [_I64, _PP, _PP, _I64P, _INT, _P]),
     "aegkv_transfer_entries": (
         _INT,
@@ -109,13 +119,16 @@ _SIGNATURES = {
     "aegkv_host_alloc": (_INT, [_PP, _I64]),
     "aegkv_host_alloc_flags": (_INT, [_PP, _I64, _INT]),
     "aegkv_host_free": (_INT, [_P]),
-    "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P]),
+    "aegkv_host_usage": (_INT, [_I64P, _I64P]),
+    "aegkv_fence_signal": (_INT, [_P, ctypes.c_uint64, _P, _P]),
     "aegkv_fence_wait": (_INT, [_P, ctypes.c_uint64, _I64, _P, _P]),
-    "aegkv_fence_publish": (_INT, [_P, ctypes.c_uint64, _P]),
+    "aegkv_fence_publish": (_INT, [_P, ctypes.c_uint64, _P, _P]),
     "aegkv_fence_host_wait": (_INT, [_P, ctypes.c_uint64, _I64]),
+    "aegkv_guard_merge": (_INT, [_P, _P, _P]),
     "aegkv_stream_create": (_INT, [_PP]),
     "aegkv_stream_create_masked": (_INT, [_PP, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int32]),
     "aegkv_stream_destroy": (_INT, [_P]),
+    "aegkv_stream_release": (_INT, [_P]),
 }
 
 _lib = None
@@ -128,6 +141,13 @@ class AegkvError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"libaegkv status {status}: {message}")
         self.status = status
+
+
+class MoveFailedError(RuntimeError):
+    """A move's completion carries the failure mark: a fence wait on its
+    stream gave up, or a move it waited for had failed, so it moved nothing
+    (or, for a STAGED swap-out, left its target host pages undefined). The
+    reference stops the worker in that case (aegaeon/worker.py:2364-2368)."""
 
 
 def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
@@ -152,6 +172,12 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
         ver = lib.aegkv_abi_version()
         if ver != ABI_VERSION:
             raise ImportError(f"libaegkv ABI {ver} != expected {ABI_VERSION}")
+        # per-device set-up before any call can be captured into a graph
+        # (a no-op without a device)
+        if torch.cuda.is_available():
+            rc = lib.aegkv_init()
+            if rc != 0:
+                raise AegkvError(rc, lib.aegkv_last_error().decode(errors="replace"))
         _lib = lib
         return lib
 

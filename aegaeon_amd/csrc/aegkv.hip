@@ -247,6 +247,15 @@ __device__ __forceinline__ void move_chunk16(const char* src, char* dst, uint32_
   }
 }
 
+// A move guard is a word a stream's fence waits set when they give up or
+// see a failed source (aegkv_fence_wait). Guarded kernels read it once at
+// the start, at system scope (it may live in pinned host memory), and move
+// nothing when it is set.
+__device__ __forceinline__ bool guard_set(const uint64_t* guard) {
+  return guard != nullptr &&
+         __hip_atomic_load(guard, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) != 0;
+}
+
 // Byte-granular fallback for callers whose offsets are not 16 B aligned.
 template <int WG>
 __device__ __forceinline__ void move_chunk_bytes(const char* src, char* dst, uint32_t nbytes) {
@@ -257,13 +266,16 @@ __device__ __forceinline__ void move_chunk_bytes(const char* src, char* dst, uin
 
 // Swap tile mover. Item w -> (entry e, segment s, chunk c), entry-major.
 // TO_HOST: device tile -> host side; otherwise host side -> device tile.
-// The host checks num_items < 2^32 so item decoding stays 32-bit.
+// The host keeps num_items + gridDim.x below 2^32 (items_fit_launch), so the
+// 32-bit grid-stride loop never wraps.
 template <int WG, int U, bool TO_HOST, bool VEC, bool NT_STORE>
 __global__ __launch_bounds__(WG) void swap_tiles_kernel(
     const SegDesc* __restrict__ segs, const EntDesc* __restrict__ ents,
     const int64_t* __restrict__ kpp, uint32_t num_segs, uint32_t num_items,
-    uint32_t chunks_per_tile, char* host_base, int64_t host_stride, int64_t host_rank_offset) {
+    uint32_t chunks_per_tile, char* host_base, int64_t host_stride, int64_t host_rank_offset,
+    const uint64_t* guard) {
   constexpr int64_t kChunk = Shape<WG, U>::kChunk;
+  if (guard_set(guard)) return;
   for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
     const uint32_t tile = w / chunks_per_tile;
     const uint32_t c = w - tile * chunks_per_tile;
@@ -294,8 +306,9 @@ __global__ __launch_bounds__(WG) void swap_tiles_kernel(
 template <int WG, int U, bool VEC, bool NT_STORE>
 __global__ __launch_bounds__(WG) void copy_blocks_kernel(
     const CopySeg* __restrict__ segs, const PairDesc* __restrict__ pairs, uint32_t num_segs,
-    uint32_t num_items, uint32_t chunks_per_tile) {
+    uint32_t num_items, uint32_t chunks_per_tile, const uint64_t* guard) {
   constexpr int64_t kChunk = Shape<WG, U>::kChunk;
+  if (guard_set(guard)) return;
   for (uint32_t w = blockIdx.x; w < num_items; w += gridDim.x) {
     const uint32_t tile = w / chunks_per_tile;
     const uint32_t c = w - tile * chunks_per_tile;
@@ -462,7 +475,11 @@ bool valid_copy_unroll(int64_t u) {
 
 // Stream-ordered pinned->device upload ring for call descriptors. A region
 // is reused only after the event recorded behind the call that read it has
-// completed, whatever stream that call ran on.
+// completed, whatever stream that call ran on. Every event remembers the
+// stream it was last recorded on, so that a stream about to be destroyed
+// can take its events with it (forget_stream): an event is never queried,
+// waited on or re-recorded after the stream that recorded it is gone. A
+// region whose event was dropped that way (ev == nullptr) has completed.
 struct Ring {
   char* host = nullptr;
   char* dev = nullptr;
@@ -471,9 +488,14 @@ struct Ring {
   struct Region {
     size_t begin, end;
     hipEvent_t ev;
+    hipStream_t stream;
+  };
+  struct Spare {
+    hipEvent_t ev;
+    hipStream_t last;  // stream it was last recorded on
   };
   std::deque<Region> inflight;
-  std::vector<hipEvent_t> spare;
+  std::vector<Spare> spare;
 };
 
 constexpr int kMaxDmaStreams = 4;
@@ -491,6 +513,8 @@ struct DeviceCtx {
   // instead of 56 ms).
   // A staged call holds the set's mutex from its first fork to its last
   // join, so its events are not re-recorded by another call in between.
+  // fork_ev and kernel_ev are recorded on callers' streams; fork_on and
+  // kernel_on name the stream of their last record (forget_stream).
   struct DmaSet {
     std::mutex mu;
     int streams = 0;
@@ -498,6 +522,8 @@ struct DeviceCtx {
     hipEvent_t fork_ev = nullptr;
     hipEvent_t join_ev[2][kMaxDmaStreams] = {};  // copies done, per staging buffer
     hipEvent_t kernel_ev[2] = {};                // gather / scatter done, per staging buffer
+    hipStream_t fork_on = nullptr;
+    hipStream_t kernel_on[2] = {};
   } dma[2];
 };
 
@@ -505,9 +531,19 @@ std::mutex g_ctx_mu;
 std::map<int, DeviceCtx*> g_ctx;
 
 std::mutex g_host_mu;
-std::map<uintptr_t, size_t> g_host_allocs;  // pools from aegkv_host_alloc(_flags)
-std::map<uintptr_t, size_t> g_uncached;     // every uncached pool: base -> allocated bytes
-std::multimap<size_t, uintptr_t> g_parked;  // released uncached pools, by size
+std::map<uintptr_t, size_t> g_host_allocs;  // live pools: start -> bytes asked for
+// Uncached host memory is never returned to the runtime. Every uncached
+// block hipHostMalloc gave stays mapped until the process ends, and live
+// uncached pools are carved out of those blocks: a freed pool's range goes
+// back to a free list (coalesced with its free neighbours in the same
+// block), and a later uncached pool takes the smallest free range that fits
+// before any new block is allocated. A process whose pools come and go in
+// different sizes thus pins no more than its largest set of live pools,
+// which keeps it under the host's cap on pinned memory.
+constexpr size_t kHostPage = 4096;
+std::map<uintptr_t, size_t> g_uncached_blocks;  // block base -> bytes
+std::map<uintptr_t, size_t> g_uncached_pools;   // live pool start -> bytes carved
+std::map<uintptr_t, size_t> g_uncached_free;    // free range start -> bytes
 
 int get_ctx(DeviceCtx** out) {
   int dev = -1;
@@ -549,13 +585,33 @@ int refuse_capture(hipStream_t stream) {
   return 0;
 }
 
+// Hand a completed region's event back to the spare list (caller holds
+// ctx->mu; the region is popped by the caller).
+void ring_retire(Ring& r, const Ring::Region& reg) {
+  if (reg.ev) r.spare.push_back({reg.ev, reg.stream});
+}
+
+// True once the oldest region's reader has finished (never blocks).
+bool ring_front_done(Ring& r) {
+  const Ring::Region& f = r.inflight.front();
+  return f.ev == nullptr || hipEventQuery(f.ev) == hipSuccess;
+}
+
+// Wait for the oldest region's reader, then retire it.
+int ring_wait_front(Ring& r) {
+  const Ring::Region f = r.inflight.front();
+  if (f.ev) AEGKV_HIP(hipEventSynchronize(f.ev));
+  ring_retire(r, f);
+  r.inflight.pop_front();
+  return 0;
+}
+
 int ring_grow(Ring& r, size_t need) {
   // Retire everything, then replace the buffers.
-  for (auto& reg : r.inflight) {
-    AEGKV_HIP(hipEventSynchronize(reg.ev));
-    r.spare.push_back(reg.ev);
+  while (!r.inflight.empty()) {
+    int rc = ring_wait_front(r);
+    if (rc) return rc;
   }
-  r.inflight.clear();
   if (r.host) AEGKV_HIP(hipHostFree(r.host));
   if (r.dev) AEGKV_HIP(hipFree(r.dev));
   r.host = nullptr;
@@ -578,8 +634,8 @@ int ring_reserve(Ring& r, size_t bytes, size_t* offset) {
     if (rc) return rc;
   }
   // Retire completed regions without blocking.
-  while (!r.inflight.empty() && hipEventQuery(r.inflight.front().ev) == hipSuccess) {
-    r.spare.push_back(r.inflight.front().ev);
+  while (!r.inflight.empty() && ring_front_done(r)) {
+    ring_retire(r, r.inflight.front());
     r.inflight.pop_front();
   }
   size_t start = r.head;
@@ -594,9 +650,8 @@ int ring_reserve(Ring& r, size_t bytes, size_t* offset) {
         break;
       }
     if (!any) break;
-    AEGKV_HIP(hipEventSynchronize(r.inflight.front().ev));
-    r.spare.push_back(r.inflight.front().ev);
-    r.inflight.pop_front();
+    int rc = ring_wait_front(r);
+    if (rc) return rc;
   }
   r.head = end;
   *offset = start;
@@ -606,19 +661,67 @@ int ring_reserve(Ring& r, size_t bytes, size_t* offset) {
 int ring_commit(Ring& r, size_t offset, size_t bytes, hipStream_t stream) {
   bytes = (bytes + 255) & ~size_t(255);
   if (bytes == 0) bytes = 256;
-  hipEvent_t ev;
+  Ring::Spare sp{nullptr, nullptr};
   if (!r.spare.empty()) {
-    ev = r.spare.back();
+    sp = r.spare.back();
     r.spare.pop_back();
   } else {
-    AEGKV_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    AEGKV_HIP(hipEventCreateWithFlags(&sp.ev, hipEventDisableTiming));
   }
-  hipError_t e = hipEventRecord(ev, stream);
+  hipError_t e = hipEventRecord(sp.ev, stream);
   if (e != hipSuccess) {
-    r.spare.push_back(ev);
+    r.spare.push_back(sp);
     return hip_fail(e, "hipEventRecord");
   }
-  r.inflight.push_back({offset, offset + bytes, ev});
+  r.inflight.push_back({offset, offset + bytes, sp.ev, stream});
+  return 0;
+}
+
+// Drop every event this library last recorded on `stream`, which the caller
+// has synchronized and is about to destroy: ring regions it read are
+// complete (their events are destroyed and the regions count as done),
+// spare events recorded there are destroyed, and the DMA sets' fork and
+// kernel events are replaced by fresh ones.
+int forget_stream(hipStream_t stream) {
+  std::vector<DeviceCtx*> ctxs;
+  {
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    for (auto& kv : g_ctx) ctxs.push_back(kv.second);
+  }
+  for (DeviceCtx* ctx : ctxs) {
+    {
+      std::lock_guard<std::mutex> lk(ctx->mu);
+      Ring& r = ctx->ring;
+      for (Ring::Region& g : r.inflight)
+        if (g.ev && g.stream == stream) {
+          (void)hipEventDestroy(g.ev);
+          g.ev = nullptr;
+        }
+      auto keep = r.spare.begin();
+      for (auto it = r.spare.begin(); it != r.spare.end(); ++it) {
+        if (it->last == stream)
+          (void)hipEventDestroy(it->ev);
+        else
+          *keep++ = *it;
+      }
+      r.spare.erase(keep, r.spare.end());
+    }
+    for (DeviceCtx::DmaSet& d : ctx->dma) {
+      std::lock_guard<std::mutex> lk(d.mu);
+      auto renew = [&](hipEvent_t* ev, hipStream_t* on) -> int {
+        if (*ev == nullptr || *on != stream) return 0;
+        (void)hipEventDestroy(*ev);
+        *ev = nullptr;
+        *on = nullptr;
+        AEGKV_HIP(hipEventCreateWithFlags(ev, hipEventDisableTiming));
+        return 0;
+      };
+      int rc = renew(&d.fork_ev, &d.fork_on);
+      for (int b = 0; b < 2 && !rc; ++b) rc = renew(&d.kernel_ev[b], &d.kernel_on[b]);
+      if (rc) return rc;
+    }
+  }
+  (void)hipGetLastError();
   return 0;
 }
 
@@ -678,11 +781,10 @@ int check_host_range(const void* ptr, int64_t bytes, const char* what) {
 bool in_uncached_pool(const void* p) {
   std::lock_guard<std::mutex> lk(g_host_mu);
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  auto it = g_uncached.upper_bound(a);
-  if (it == g_uncached.begin()) return false;
+  auto it = g_uncached_pools.upper_bound(a);
+  if (it == g_uncached_pools.begin()) return false;
   --it;
-  return a >= it->first && a < it->first + it->second &&
-         g_host_allocs.count(it->first) != 0;
+  return a < it->first + it->second;
 }
 
 // ----------------------------------------------------------- launching --
@@ -698,6 +800,30 @@ int64_t launch_grid(int64_t limit, int64_t items, int lanes) {
   return std::max<int64_t>(1, std::min<int64_t>(g, cap));
 }
 
+// Work items one launch may hold. The kernels walk items with a 32-bit
+// grid-stride loop (w += gridDim.x) and launch_grid caps a grid at
+// (2^32 - 1) / lanes workgroups, so with lanes >= 256 and at most this many
+// items, w + gridDim.x stays below 2^32 and the loop never wraps.
+constexpr int64_t kMaxLaunchItems =
+    static_cast<int64_t>(UINT32_MAX) - static_cast<int64_t>(UINT32_MAX) / 256;
+
+// a * b * c work items, or -1 when that exceeds kMaxLaunchItems (or overflows).
+int64_t launch_items(int64_t a, int64_t b, int64_t c) {
+  if (a < 0 || b < 0 || c < 0) return -1;
+  if (a == 0 || b == 0 || c == 0) return 0;
+  if (a > kMaxLaunchItems / b) return -1;
+  const int64_t ab = a * b;
+  if (ab > kMaxLaunchItems / c) return -1;
+  return ab * c;
+}
+
+int too_many_items(int64_t a, int64_t b, int64_t c, const char* what) {
+  return fail(AEGKV_EINVAL, "%lld %s x %lld segments x %lld chunks exceed the %lld work items "
+              "of one launch; split the call", static_cast<long long>(a), what,
+              static_cast<long long>(b), static_cast<long long>(c),
+              static_cast<long long>(kMaxLaunchItems));
+}
+
 struct SwapArgs {
   const SegDesc* segs;
   const EntDesc* ents;
@@ -705,6 +831,7 @@ struct SwapArgs {
   uint32_t num_segs, num_items, cpt;
   char* host_base;
   int64_t host_stride, host_rank_offset;
+  const uint64_t* guard;
 };
 
 template <int WG, int U, bool TO_HOST, bool VEC, bool NT>
@@ -713,7 +840,7 @@ hipError_t launch_swap_t(int64_t grid, hipStream_t st, const SwapArgs& a) {
   hipLaunchKernelGGL((swap_tiles_kernel<WG, U, TO_HOST, VEC, NT>),
                      dim3(static_cast<uint32_t>(grid)), dim3(WG), 0, st, a.segs, a.ents, a.kpp,
                      a.num_segs, a.num_items, a.cpt, a.host_base, a.host_stride,
-                     a.host_rank_offset);
+                     a.host_rank_offset, a.guard);
   return hipGetLastError();
 }
 
@@ -745,21 +872,22 @@ hipError_t launch_swap(ShapeSel sh, bool to_host, bool vec, bool nt, int64_t gri
 // caps how many workgroups share a CU.
 template <int WG, int U, bool VEC, bool NT>
 hipError_t launch_copy_t(int64_t grid, unsigned lds, hipStream_t st, const CopySeg* s,
-                         const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt) {
+                         const PairDesc* p, uint32_t ns, uint32_t items, uint32_t cpt,
+                         const uint64_t* guard) {
   (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL((copy_blocks_kernel<WG, U, VEC, NT>), dim3(static_cast<uint32_t>(grid)),
-                     dim3(WG), lds, st, s, p, ns, items, cpt);
+                     dim3(WG), lds, st, s, p, ns, items, cpt, guard);
   return hipGetLastError();
 }
 
 hipError_t launch_copy(ShapeSel sh, bool vec, bool nt, int64_t grid, unsigned lds,
                        hipStream_t st, const CopySeg* s, const PairDesc* p, uint32_t ns,
-                       uint32_t items, uint32_t cpt) {
-  if (!vec) return launch_copy_t<256, 1, false, false>(grid, 0, st, s, p, ns, items, cpt);
+                       uint32_t items, uint32_t cpt, const uint64_t* guard) {
+  if (!vec) return launch_copy_t<256, 1, false, false>(grid, 0, st, s, p, ns, items, cpt, guard);
 #define AEGKV_CP(W, UU)                                                               \
   if (sh.wg == W && sh.u == UU)                                                       \
-    return nt ? launch_copy_t<W, UU, true, true>(grid, lds, st, s, p, ns, items, cpt) \
-              : launch_copy_t<W, UU, true, false>(grid, lds, st, s, p, ns, items, cpt);
+    return nt ? launch_copy_t<W, UU, true, true>(grid, lds, st, s, p, ns, items, cpt, guard) \
+              : launch_copy_t<W, UU, true, false>(grid, lds, st, s, p, ns, items, cpt, guard);
   AEGKV_CP(256, 1) AEGKV_CP(256, 2) AEGKV_CP(256, 4) AEGKV_CP(256, 8)
   AEGKV_CP(1024, 1) AEGKV_CP(1024, 2) AEGKV_CP(1024, 3) AEGKV_CP(1024, 4)
   AEGKV_CP(1024, 5) AEGKV_CP(1024, 6) AEGKV_CP(1024, 8) AEGKV_CP(1024, 10)
@@ -837,6 +965,7 @@ struct SwapList {
   const int32_t* group;     // may be null: all group 0
   const int64_t* first;     // may be null: all 0
   const int64_t* valid;     // may be null: all kpp[group]
+  const uint64_t* guard;    // may be null: the kernels move nothing once *guard != 0
 };
 
 bool mul_fits(int64_t a, int64_t b) { return a >= 0 && b >= 0 && (b == 0 || a <= INT64_MAX / b); }
@@ -954,6 +1083,15 @@ int validate_list(const SwapLayout& L, const SwapList& E, bool is_swap_in) {
   return 0;
 }
 
+// Launch shape of the swap kernels: 256 lanes with the tuned loads per
+// lane, or (tuning key 8) the copy's page-sized shape; bytes alone on the
+// unaligned path.
+ShapeSel swap_shape(const Tunables& t, bool vec, int64_t max_page) {
+  if (!vec) return ShapeSel{256, 1};
+  return t.swap_shape_auto ? auto_shape(max_page)
+                           : ShapeSel{256, static_cast<int>(t.swap_unroll)};
+}
+
 struct Run {
   int64_t host_off;   // byte offset inside the host pool
   int64_t stage_off;  // byte offset inside staging
@@ -1004,22 +1142,19 @@ int enqueue_swap_kernel(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
   }
   char* dv = ctx->ring.dev + off;
   const Tunables t = tunables();
-  const ShapeSel sh = !vec ? ShapeSel{256, 1}
-                           : (t.swap_shape_auto ? auto_shape(max_page)
-                                                : ShapeSel{256, static_cast<int>(t.swap_unroll)});
+  const ShapeSel sh = swap_shape(t, vec, max_page);
   const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
-  const int64_t items = n * S * cpt;
-  if (items >= (int64_t(1) << 32)) {
+  const int64_t items = launch_items(n, S, cpt);
+  if (items < 0) {
     ctx->ring.head = off;  // nothing was enqueued; hand the region back
-    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
-                static_cast<long long>(items));
+    return too_many_items(n, S, cpt, "entries");
   }
   hipError_t e = hipMemcpyAsync(dv, h, total, hipMemcpyHostToDevice, stream);
   if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptor)");
   SwapArgs a{reinterpret_cast<const SegDesc*>(dv), reinterpret_cast<const EntDesc*>(dv + ent_off),
              reinterpret_cast<const int64_t*>(dv + kpp_off), static_cast<uint32_t>(S),
              static_cast<uint32_t>(items), static_cast<uint32_t>(cpt), host_side, host_stride,
-             host_rank_off};
+             host_rank_off, E.guard};
   // Non-temporal stores only where the destination is HBM: plain stores to
   // the host pool measured faster (no L2 residency to avoid there).
   const bool nt = t.nt_stores != 0 && !(!is_swap_in && !staged);
@@ -1156,6 +1291,7 @@ int chunk_copies(DeviceCtx* ctx, int k, const std::vector<Run>& runs, bool to_de
   std::lock_guard<std::mutex> lk(d.mu);
   int rc = ensure_dma(d, k);
   if (rc) return rc;
+  d.fork_on = stream;
   AEGKV_HIP(hipEventRecord(d.fork_ev, stream));
   for (int j = 0; j < k; ++j) AEGKV_HIP(hipStreamWaitEvent(d.st[j], d.fork_ev, 0));
   rc = runs_on_dma(d, k, runs, to_device, staging, host, d.join_ev[0]);
@@ -1242,8 +1378,9 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
     (void)hipGetLastError();
     return status;
   };
-  // every DMA stream waits `ev`, recorded on `on`
-  auto fan_in = [&](hipEvent_t ev, hipStream_t on) {
+  // every DMA stream waits `ev`, recorded on `on` (which *ev_on notes)
+  auto fan_in = [&](hipEvent_t ev, hipStream_t* ev_on, hipStream_t on) {
+    *ev_on = on;
     hipError_t e = hipEventRecord(ev, on);
     for (int j = 0; j < k && e == hipSuccess; ++j) e = hipStreamWaitEvent(d.st[j], ev, 0);
     return e;
@@ -1254,7 +1391,7 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
     for (int j = 0; j < k && e == hipSuccess; ++j) e = hipStreamWaitEvent(stream, d.join_ev[b][j], 0);
     return e;
   };
-  hipError_t e = fan_in(d.fork_ev, stream);
+  hipError_t e = fan_in(d.fork_ev, &d.fork_on, stream);
   if (e != hipSuccess) return unwind(hip_fail(e, "staged fork"));
   std::vector<Run> runs;
   for (size_t c = 0; c < chunks; ++c) {
@@ -1269,7 +1406,7 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
       rc = staged_kernel(ctx, L, E, order, lo, hi, false, buf[b], composite, vec_stage,
                          runs.size(), t, stream);
       if (rc) return unwind(rc);
-      if ((e = fan_in(d.kernel_ev[b], stream)) != hipSuccess)
+      if ((e = fan_in(d.kernel_ev[b], &d.kernel_on[b], stream)) != hipSuccess)
         return unwind(hip_fail(e, "staged gather event"));
       rc = runs_on_dma(d, k, runs, false, buf[b], L.host_pool, d.join_ev[b]);
       if (rc) return unwind(rc);
@@ -1284,6 +1421,7 @@ int staged_overlapped(DeviceCtx* ctx, const SwapLayout& L, const SwapList& E,
       rc = staged_kernel(ctx, L, E, order, lo, hi, true, buf[b], composite, vec_stage,
                          runs.size(), t, stream);
       if (rc) return unwind(rc);
+      d.kernel_on[b] = stream;
       if ((e = hipEventRecord(d.kernel_ev[b], stream)) != hipSuccess)
         return unwind(hip_fail(e, "staged scatter event"));
     }
@@ -1310,6 +1448,16 @@ int swap_core(const SwapLayout& L, const SwapList& E, bool is_swap_in, int mode,
   rc = validate_list(L, E, is_swap_in);
   if (rc) return rc;
   if (E.n == 0) return 0;
+  {
+    // the whole list in one launch (a staged chunk holds fewer entries)
+    int64_t max_page = 0;
+    for (int32_t s = 0; s < L.num_segments; ++s) max_page = std::max(max_page, L.page_bytes[s]);
+    const bool vec = staged ? dev_vec && composite % 16 == 0 : dev_vec && host_vec;
+    const ShapeSel sh = swap_shape(t, vec, max_page);
+    const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
+    if (launch_items(E.n, L.num_segments, cpt) < 0)
+      return too_many_items(E.n, L.num_segments, cpt, "entries");
+  }
   rc = check_layout_pointers(L);
   if (rc) return rc;
   rc = refuse_capture(stream);
@@ -1482,10 +1630,8 @@ int copy_plan(const Tunables& t, bool vec, int64_t max_page, int32_t num_segment
     sh = ShapeSel{t.copy_lanes == 256 ? 256 : 1024, static_cast<int>(t.copy_unroll)};
   if (!vec) sh = ShapeSel{256, 1};
   const int64_t cpt = (max_page + sh.chunk() - 1) / sh.chunk();
-  const int64_t items = num_pairs * num_segments * cpt;
-  if (items >= (int64_t(1) << 32))
-    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
-                static_cast<long long>(items));
+  const int64_t items = launch_items(num_pairs, num_segments, cpt);
+  if (items < 0) return too_many_items(num_pairs, num_segments, cpt, "pairs");
   *out = CopyPlan{sh, vec, cpt, items};
   return 0;
 }
@@ -1506,12 +1652,14 @@ void pack_copy_desc(char* h, int32_t num_segments, void* const* src_bases,
   for (int64_t i = 0; i < num_pairs; ++i) hp[i] = PairDesc{src_ids[i], dst_ids[i]};
 }
 
-// What a copy call launches: the copy itself, or one of its measurement
-// twins (aegkv_copy_probe) with the sink word and magic they take.
+// What a copy call launches: the copy itself (guarded by `guard` when it is
+// not null), or one of its measurement twins (aegkv_copy_probe) with the
+// sink word and magic they take.
 struct CopyKind {
   int probe = 0;            // 0 = copy, PROBE_READ or PROBE_WRITE
   uint32_t* sink = nullptr;
   uint32_t magic = 0;
+  const uint64_t* guard = nullptr;
 };
 
 // Launch the copy kernel (or a probe twin) over descriptors already on the
@@ -1530,7 +1678,7 @@ hipError_t copy_launch(const CopyPlan& p, const Tunables& t, int num_cus, int32_
     return launch_probe(p.sh, kind.probe, t.nt_stores != 0, grid, lds, stream, segs, pairs, ns,
                         items, cpt, kind.sink, kind.magic);
   return launch_copy(p.sh, p.vec, t.nt_stores != 0, grid, lds, stream, segs, pairs, ns, items,
-                     cpt);
+                     cpt, kind.guard);
 }
 
 int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bases,
@@ -1548,12 +1696,12 @@ int copy_core(int32_t num_segments, void* const* src_bases, void* const* dst_bas
   if (kind.probe && !vec)
     return fail(AEGKV_EINVAL, "the probes move 16 B per lane: bases and pages must be "
                 "16 B multiples");
-  rc = copy_check_device(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
-                         dst_num_blocks, same_cache);
-  if (rc) return rc;
   const Tunables t = tunables();
   CopyPlan plan;
   rc = copy_plan(t, vec, max_page, num_segments, num_pairs, &plan);
+  if (rc) return rc;
+  rc = copy_check_device(num_segments, src_bases, dst_bases, page_bytes, src_num_blocks,
+                         dst_num_blocks, same_cache);
   if (rc) return rc;
   rc = refuse_capture(stream);
   if (rc) return rc;
@@ -1608,19 +1756,37 @@ int g_noalloc_cus[kNoAllocMaxDevices] = {};
 alignas(256) unsigned char g_noalloc_host[kNoAllocBytes];  // descriptor packing (pageable)
 int64_t g_noalloc_work[2][kNoAllocMaxPairs];    // sorted id copies for the checks
 
-// Device address of this device's `scratch` (caller holds g_noalloc_mu).
-// hipGetSymbolAddress runs once per device, with that device current.
-int noalloc_scratch(int dev, char** out, int* num_cus) {
+// Looks up this device's `scratch` address and CU count, once per device,
+// with that device current (caller holds g_noalloc_mu). aegkv_init does it
+// for every device at set-up.
+int noalloc_resolve(int dev) {
   if (dev < 0 || dev >= kNoAllocMaxDevices)
     return fail(AEGKV_EINVAL, "device %d is outside the %d devices the allocation-free "
                 "copy supports", dev, kNoAllocMaxDevices);
-  if (!g_scratch_ptr[dev]) {
-    void* p = nullptr;
-    AEGKV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-    int cus = 0;
-    AEGKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    g_noalloc_cus[dev] = cus > 0 ? cus : 1;
-    g_scratch_ptr[dev] = static_cast<char*>(p);
+  if (g_scratch_ptr[dev]) return 0;
+  void* p = nullptr;
+  AEGKV_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  int cus = 0;
+  AEGKV_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  g_noalloc_cus[dev] = cus > 0 ? cus : 1;
+  g_scratch_ptr[dev] = static_cast<char*>(p);
+  return 0;
+}
+
+// Device address of the current device's `scratch` (caller holds
+// g_noalloc_mu). Without aegkv_init, the first call on a device looks it
+// up, unless that call's stream is being captured: the lookup may load the
+// library's code object, which must not happen inside a capture.
+int noalloc_scratch(int dev, hipStream_t stream, char** out, int* num_cus) {
+  if (dev < 0 || dev >= kNoAllocMaxDevices || !g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &status);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (status != hipStreamCaptureStatusNone)
+      return fail(AEGKV_EINVAL, "the allocation-free copy's first call on device %d is being "
+                  "captured; call aegkv_init() before capturing", dev);
+    int rc = noalloc_resolve(dev);
+    if (rc) return rc;
   }
   *out = g_scratch_ptr[dev];
   *num_cus = g_noalloc_cus[dev];
@@ -1665,17 +1831,17 @@ int copy_noalloc(int32_t num_segments, void* const* bases, const int64_t* page_b
   rc = copy_check_ids_sorted(num_pairs, src_ids, dst_ids, true, g_noalloc_work[0],
                              g_noalloc_work[1]);
   if (rc || num_pairs == 0) return rc;
-  rc = copy_check_device(num_segments, bases, bases, page_bytes, num_blocks, num_blocks, true);
-  if (rc) return rc;
   const Tunables t = tunables();
   CopyPlan plan;
   rc = copy_plan(t, vec, max_page, num_segments, num_pairs, &plan);
+  if (rc) return rc;
+  rc = copy_check_device(num_segments, bases, bases, page_bytes, num_blocks, num_blocks, true);
   if (rc) return rc;
   int dev = -1;
   AEGKV_HIP(hipGetDevice(&dev));
   char* dv = nullptr;
   int num_cus = 0;
-  rc = noalloc_scratch(dev, &dv, &num_cus);
+  rc = noalloc_scratch(dev, stream, &dv, &num_cus);
   if (rc) return rc;
   pack_copy_desc(reinterpret_cast<char*>(g_noalloc_host), num_segments, bases, bases,
                  page_bytes, num_pairs, src_ids, dst_ids);
@@ -1725,6 +1891,14 @@ int slices_core(int64_t n, void* const* dst, const void* const* src, const int64
                   static_cast<long long>(a), static_cast<long long>(b));
   }
   if (keep.empty()) return 0;
+  const int64_t chunk = vec ? int64_t(256) * 16 * 2 : int64_t(256) * 16;
+  int64_t items = 0;
+  for (int64_t i : keep) {
+    items += (bytes[i] + chunk - 1) / chunk;
+    if (items > kMaxLaunchItems)
+      return fail(AEGKV_EINVAL, "the slices need more than the %lld work items of one launch; "
+                  "split the call", static_cast<long long>(kMaxLaunchItems));
+  }
   for (int64_t i : keep) {
     int rc = check_device_range(dst[i], bytes[i], "target slice");
     if (!rc) rc = check_host_range(src[i], bytes[i], "source slice");
@@ -1737,12 +1911,6 @@ int slices_core(int64_t n, void* const* dst, const void* const* src, const int64
                                hipMemcpyHostToDevice, stream));
     return 0;
   }
-  const int64_t chunk = vec ? int64_t(256) * 16 * 2 : int64_t(256) * 16;
-  int64_t items = 0;
-  for (int64_t i : keep) items += (bytes[i] + chunk - 1) / chunk;
-  if (items >= (int64_t(1) << 32) || keep.size() >= (size_t(1) << 32))
-    return fail(AEGKV_EINVAL, "%lld work items exceed one launch; split the call",
-                static_cast<long long>(items));
   int rc = refuse_capture(stream);
   if (rc) return rc;
   DeviceCtx* ctx = nullptr;
@@ -1864,7 +2032,7 @@ int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
   const int64_t kpp[1] = {1};
   SwapLayout L{1, bases, page, hoff, owner, cache_num_blocks, 1, kpp,
                static_cast<char*>(kv_swap), swap_num_blocks, block_bytes, 0};
-  SwapList E{num_ids, source_block_ids, target_block_ids, nullptr, nullptr, nullptr};
+  SwapList E{num_ids, source_block_ids, target_block_ids, nullptr, nullptr, nullptr, nullptr};
   return swap_core(L, E, is_swap_in != 0, mode, stream);
 }
 
@@ -1877,17 +2045,19 @@ int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
                       const int64_t* source_block_ids, const int64_t* target_block_ids,
                       const int32_t* group_ids, const int64_t* first_kernel_blocks,
                       const int64_t* valid_kernel_blocks, int is_swap_in, int mode,
-                      hipStream_t stream) {
+                      const uint64_t* guard, hipStream_t stream) {
   g_err[0] = '\0';
   if (int rc = env_status()) return rc;
   if (num_entries > 0 && (!group_ids || !first_kernel_blocks || !valid_kernel_blocks))
     return fail(AEGKV_EINVAL, "entry metadata arrays must not be null");
+  if (guard && (reinterpret_cast<uintptr_t>(guard) & 7u))
+    return fail(AEGKV_EINVAL, "the move guard must be an 8-byte aligned word");
   SwapLayout L{num_segments, segment_bases, segment_page_bytes, segment_host_offsets,
                segment_owner_masks, device_num_blocks, num_groups,
                group_kernel_blocks_per_page, static_cast<char*>(host_pool), host_num_blocks,
                host_page_bytes, host_rank_offset};
   SwapList E{num_entries, source_block_ids, target_block_ids, group_ids, first_kernel_blocks,
-             valid_kernel_blocks};
+             valid_kernel_blocks, guard};
   return swap_core(L, E, is_swap_in != 0, mode, stream);
 }
 
@@ -1937,14 +2107,18 @@ int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
                          void* const* dst_segment_bases, const int64_t* segment_page_bytes,
                          int64_t src_num_blocks, int64_t dst_num_blocks, int64_t num_pairs,
                          const int64_t* src_block_ids, const int64_t* dst_block_ids,
-                         hipStream_t stream) {
+                         const uint64_t* guard, hipStream_t stream) {
   g_err[0] = '\0';
   if (int rc = env_status()) return rc;
   if (!src_segment_bases || !dst_segment_bases)
     return fail(AEGKV_EINVAL, "segment arrays must not be null");
+  if (guard && (reinterpret_cast<uintptr_t>(guard) & 7u))
+    return fail(AEGKV_EINVAL, "the move guard must be an 8-byte aligned word");
+  CopyKind k;
+  k.guard = guard;
   return copy_core(num_segments, src_segment_bases, dst_segment_bases, segment_page_bytes,
                    src_num_blocks, dst_num_blocks, num_pairs, src_block_ids, dst_block_ids,
-                   false, stream);
+                   false, stream, k);
 }
 
 int aegkv_load_slices(int64_t num_slices, void* const* dst, const void* const* src,
@@ -1989,13 +2163,46 @@ int aegkv_stream_create_masked(hipStream_t* stream, const uint32_t* cu_mask,
   return 0;
 }
 
-int aegkv_stream_destroy(hipStream_t stream) {
+int aegkv_stream_release(hipStream_t stream) {
   g_err[0] = '\0';
   if (!stream) return fail(AEGKV_EINVAL, "stream must not be null");
-  // the stream's queued work finishes first, whatever the caller dropped
   AEGKV_HIP(hipStreamSynchronize(stream));
+  return forget_stream(stream);
+}
+
+int aegkv_stream_destroy(hipStream_t stream) {
+  // the stream's queued work finishes first, whatever the caller dropped,
+  // and no library event stays recorded on it
+  if (int rc = aegkv_stream_release(stream)) return rc;
   AEGKV_HIP(hipStreamDestroy(stream));
   return 0;
+}
+
+int aegkv_init(void) {
+  g_err[0] = '\0';
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    (void)hipGetLastError();
+    return 0;  // no device: nothing to set up
+  }
+  int current = -1;
+  AEGKV_HIP(hipGetDevice(&current));
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  // the current device first, with no device switch (a process with one
+  // device never switches)
+  int rc = current < kNoAllocMaxDevices ? noalloc_resolve(current) : 0;
+  bool switched = false;
+  for (int d = 0; d < count && d < kNoAllocMaxDevices && !rc; ++d) {
+    if (d == current || g_scratch_ptr[d]) continue;
+    const hipError_t e = hipSetDevice(d);
+    switched = true;
+    rc = e != hipSuccess ? hip_fail(e, "hipSetDevice") : noalloc_resolve(d);
+  }
+  if (switched) {
+    const hipError_t e = hipSetDevice(current);
+    if (!rc && e != hipSuccess) rc = hip_fail(e, "hipSetDevice");
+  }
+  return rc;
 }
 
 int aegkv_host_alloc(void** ptr, int64_t bytes) { return aegkv_host_alloc_flags(ptr, bytes, 0); }
@@ -2003,35 +2210,61 @@ int aegkv_host_alloc(void** ptr, int64_t bytes) { return aegkv_host_alloc_flags(
 int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags) {
   g_err[0] = '\0';
   if (!ptr || bytes <= 0) return fail(AEGKV_EINVAL, "host_alloc needs a pointer and bytes > 0");
-  if (flags & ~AEGKV_HOST_UNCACHED) return fail(AEGKV_EINVAL, "unknown host_alloc flags 0x%x", flags);
+  if (flags & ~(AEGKV_HOST_UNCACHED | AEGKV_HOST_COHERENT))
+    return fail(AEGKV_EINVAL, "unknown host_alloc flags 0x%x", flags);
   const size_t n = static_cast<size_t>(bytes);
-  void* p = nullptr;
-  if (flags & AEGKV_HOST_UNCACHED) {
-    // Reuse the smallest parked uncached pool that fits. Parked memory stays
-    // pinned until the process ends anyway, so a larger one costs nothing
-    // extra, and reusing it keeps the process under the host's cap on pinned
-    // memory when pools of different sizes come and go.
-    std::lock_guard<std::mutex> lk(g_host_mu);
-    auto it = g_parked.lower_bound(n);
-    if (it != g_parked.end()) {
-      p = reinterpret_cast<void*>(it->second);
-      g_parked.erase(it);
-    }
-  }
-  if (!p) {
-    unsigned hf = hipHostMallocMapped | hipHostMallocPortable;
-    if (flags & AEGKV_HOST_UNCACHED) hf |= hipHostMallocUncached;
+  const bool uncached = (flags & AEGKV_HOST_UNCACHED) != 0;
+  unsigned hf = hipHostMallocMapped | hipHostMallocPortable;
+  if (uncached) hf |= hipHostMallocUncached;
+  if (flags & AEGKV_HOST_COHERENT) hf |= hipHostMallocCoherent;
+  if (!uncached) {
+    void* p = nullptr;
     AEGKV_HIP(hipHostMalloc(&p, n, hf));
-    if (flags & AEGKV_HOST_UNCACHED) {
-      std::lock_guard<std::mutex> lk(g_host_mu);
-      g_uncached[reinterpret_cast<uintptr_t>(p)] = n;
-    }
-  }
-  {
     std::lock_guard<std::mutex> lk(g_host_mu);
     g_host_allocs[reinterpret_cast<uintptr_t>(p)] = n;
+    *ptr = p;
+    return 0;
   }
+  const size_t want = (n + kHostPage - 1) / kHostPage * kHostPage;
+  {
+    // the smallest free range that fits
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    auto best = g_uncached_free.end();
+    for (auto it = g_uncached_free.begin(); it != g_uncached_free.end(); ++it)
+      if (it->second >= want && (best == g_uncached_free.end() || it->second < best->second))
+        best = it;
+    if (best != g_uncached_free.end()) {
+      const uintptr_t start = best->first;
+      const size_t len = best->second;
+      g_uncached_free.erase(best);
+      if (len > want) g_uncached_free[start + want] = len - want;
+      g_uncached_pools[start] = want;
+      g_host_allocs[start] = n;
+      *ptr = reinterpret_cast<void*>(start);
+      return 0;
+    }
+  }
+  void* p = nullptr;
+  AEGKV_HIP(hipHostMalloc(&p, want, hf));
+  std::lock_guard<std::mutex> lk(g_host_mu);
+  const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+  g_uncached_blocks[b] = want;
+  g_uncached_pools[b] = want;
+  g_host_allocs[b] = n;
   *ptr = p;
+  return 0;
+}
+
+int aegkv_host_usage(int64_t* pinned_bytes, int64_t* uncached_free_bytes) {
+  g_err[0] = '\0';
+  std::lock_guard<std::mutex> lk(g_host_mu);
+  int64_t pinned = 0, free_bytes = 0;
+  for (const auto& kv : g_host_allocs)
+    if (!g_uncached_pools.count(kv.first)) pinned += static_cast<int64_t>(kv.second);
+  for (const auto& kv : g_uncached_blocks) pinned += static_cast<int64_t>(kv.second);
+  for (const auto& kv : g_uncached_free) free_bytes += static_cast<int64_t>(kv.second);
+  if (pinned_bytes) *pinned_bytes = pinned;
+  if (uncached_free_bytes) *uncached_free_bytes = free_bytes;
   return 0;
 }
 
@@ -2043,11 +2276,29 @@ int aegkv_host_free(void* ptr) {
     const uintptr_t b = reinterpret_cast<uintptr_t>(ptr);
     if (g_host_allocs.erase(b) == 0)
       return fail(AEGKV_EINVAL, "%p is not a live pool from aegkv_host_alloc", ptr);
-    auto u = g_uncached.find(b);
-    if (u != g_uncached.end()) {
-      // uncached pools stay mapped until the process ends; a later uncached
-      // allocation of a fitting size reuses this one
-      g_parked.emplace(u->second, b);
+    auto u = g_uncached_pools.find(b);
+    if (u != g_uncached_pools.end()) {
+      // back to the free list, merged with free neighbours of the same block
+      uintptr_t start = b;
+      size_t len = u->second;
+      g_uncached_pools.erase(u);
+      auto blk = g_uncached_blocks.upper_bound(start);
+      --blk;  // the block holding the pool (every pool lies in one)
+      const uintptr_t block_begin = blk->first, block_end = blk->first + blk->second;
+      auto next = g_uncached_free.find(start + len);
+      if (next != g_uncached_free.end() && start + len < block_end) {
+        len += next->second;
+        g_uncached_free.erase(next);
+      }
+      auto prev = g_uncached_free.lower_bound(start);
+      if (prev != g_uncached_free.begin()) {
+        --prev;
+        if (prev->first >= block_begin && prev->first + prev->second == start) {
+          prev->second += len;
+          return 0;
+        }
+      }
+      g_uncached_free[start] = len;
       return 0;
     }
   }

@@ -18,8 +18,27 @@
 //   * aegkv_fence_wait enqueues a one-wave kernel that polls a word (acquire
 //     at system scope) until it reaches a value, so every later operation on
 //     the stream runs after the signal. The poll is bounded by a wall-clock
-//     budget: a wait that runs out ends anyway and sets a caller-provided
-//     flag word to 1, so no wave ever spins forever.
+//     budget: a wait that runs out ends anyway and sets the stream's move
+//     guard (a caller-provided word) to 1, so no wave ever spins forever.
+//
+// A failed wait must not let the stream's later moves pass for good ones.
+// The reference never runs a swap before its source is ready: it waits
+// without a limit (aegaeon/worker.py:2387) and stops the worker when it
+// cannot get the source events (:2364-2368). Here the give-up is marked
+// instead, and the mark travels with everything that reports completion:
+//   * guarded moves (aegkv_swap_blocks, aegkv_migrate_blocks with a guard)
+//     read the guard first and move nothing once it is set;
+//   * a guarded signal raises its word to value | AEGKV_FENCE_FAILED, and a
+//     wait that sees that bit sets its own stream's guard to 2, so the
+//     failure follows the chain of moves across streams and processes;
+//   * a guarded publish raises its host word to value | AEGKV_FENCE_FAILED,
+//     which aegkv_fence_host_wait reports as 2 (failed), not as done;
+//   * aegkv_guard_merge sets a consumer's guard to 2 behind its stream's
+//     work when a producer's guard is set, for a consumer that waits on the
+//     producer's event instead of a fence word.
+// A failure is sticky: the mark stays in the words (atomic max) and the
+// guard is never cleared by the library, as the reference's stopped worker
+// moves nothing more.
 //
 // Every memory operation here is a vector-memory load, store or atomic.
 //
@@ -60,26 +79,51 @@ int hip_fail(hipError_t e, const char* what) {
 
 // Longest budget a wait may ask for (10 minutes).
 constexpr int64_t kMaxWaitMicros = int64_t(600) * 1000 * 1000;
+constexpr uint64_t kFailed = AEGKV_FENCE_FAILED;
 
-__global__ void __launch_bounds__(64) fence_signal_kernel(uint64_t* word, uint64_t value) {
-  if (threadIdx.x == 0)
-    (void)__hip_atomic_fetch_max(word, value, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+// Guard values a wait stores (any non-zero value stops guarded moves).
+constexpr uint64_t kGuardTimedOut = 1;
+constexpr uint64_t kGuardSourceFailed = 2;
+
+__device__ __forceinline__ uint64_t load_guard(const uint64_t* guard) {
+  return guard ? __hip_atomic_load(guard, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) : 0;
+}
+
+// Guards are set with plain stores, not read-modify-writes: they may live
+// in pinned host memory, and any non-zero value means the same thing.
+__device__ __forceinline__ void set_guard(uint64_t* guard, uint64_t why) {
+  __hip_atomic_store(guard, why, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__global__ void __launch_bounds__(64) fence_signal_kernel(uint64_t* word, uint64_t value,
+                                                          const uint64_t* guard) {
+  if (threadIdx.x != 0) return;
+  const uint64_t v = load_guard(guard) != 0 ? (value | kFailed) : value;
+  (void)__hip_atomic_fetch_max(word, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __global__ void __launch_bounds__(64) fence_wait_kernel(const uint64_t* word, uint64_t value,
-                                                        uint64_t budget_ticks,
-                                                        uint64_t* timed_out) {
+                                                        uint64_t budget_ticks, uint64_t* guard) {
   if (threadIdx.x != 0) return;
   const uint64_t start = wall_clock64();
   for (;;) {
     const uint64_t seen = __hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (seen & kFailed) {
+      set_guard(guard, kGuardSourceFailed);
+      return;
+    }
     if (seen >= value) return;
     if (wall_clock64() - start > budget_ticks) {
-      __hip_atomic_store(timed_out, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      set_guard(guard, kGuardTimedOut);
       return;
     }
     __builtin_amdgcn_s_sleep(8);
   }
+}
+
+__global__ void __launch_bounds__(64) guard_merge_kernel(uint64_t* guard, const uint64_t* source) {
+  if (threadIdx.x != 0) return;
+  if (load_guard(source) != 0) set_guard(guard, kGuardSourceFailed);
 }
 
 // A fence word must be 8-byte aligned memory the current device can access:
@@ -130,13 +174,38 @@ void host_word_max(uint64_t* word, uint64_t value) {
 struct Publish {
   uint64_t* word;
   uint64_t value;
+  const uint64_t* guard;  // host-readable, or null
 };
 
-// Runs on the runtime's host-function thread once the stream reaches it.
+// Runs on the runtime's host-function thread once the stream reaches it,
+// after every earlier operation on the stream (the guard's last writer
+// included) has finished.
 void publish_cb(void* data) {
   Publish* p = static_cast<Publish*>(data);
-  host_word_max(p->word, p->value);
+  const bool failed = p->guard && __atomic_load_n(p->guard, __ATOMIC_ACQUIRE) != 0;
+  host_word_max(p->word, failed ? (p->value | kFailed) : p->value);
   delete p;
+}
+
+// A guard the host function reads: pinned host memory.
+int check_host_guard(const uint64_t* g) {
+  if (reinterpret_cast<uintptr_t>(g) & 7u)
+    return fail(AEGKV_EINVAL, "move guard must be 8-byte aligned");
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, g);
+  if (e != hipSuccess || attr.type != hipMemoryTypeHost) {
+    (void)hipGetLastError();
+    return fail(AEGKV_EINVAL, "a published fence's move guard must be pinned host memory "
+                "(the host function reads it)");
+  }
+  return 0;
+}
+
+int check_value(uint64_t value) {
+  if (value == 0 || value >= kFailed)
+    return fail(AEGKV_EINVAL, "fence values are positive and below 2^62 (bit 62 marks a "
+                "failed move)");
+  return 0;
 }
 
 int check_host_word(const void* p) {
@@ -150,12 +219,13 @@ int check_host_word(const void* p) {
 
 extern "C" {
 
-int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream) {
+int aegkv_fence_publish(uint64_t* host_word, uint64_t value, const uint64_t* guard,
+                        hipStream_t stream) {
   aegkv_clear_error();
   int rc = check_host_word(host_word);
+  if (!rc) rc = check_value(value);
+  if (!rc && guard) rc = check_host_guard(guard);
   if (rc) return rc;
-  if (value == 0 || value >= (uint64_t(1) << 63))
-    return fail(AEGKV_EINVAL, "fence values are positive and below 2^63");
   // The callback frees its record, so a graph replaying it would use a
   // freed record: refuse a capturing stream.
   hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
@@ -163,7 +233,7 @@ int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream)
   if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
   if (status != hipStreamCaptureStatusNone)
     return fail(AEGKV_EINVAL, "fence publish cannot be captured into a graph");
-  Publish* p = new Publish{host_word, value};
+  Publish* p = new Publish{host_word, value, guard};
   e = hipLaunchHostFunc(stream, publish_cb, p);
   if (e != hipSuccess) {
     delete p;
@@ -181,7 +251,9 @@ int aegkv_fence_host_wait(const uint64_t* host_word, uint64_t value, int64_t tim
                 static_cast<long long>(timeout_us), static_cast<long long>(kMaxWaitMicros));
   const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(timeout_us);
   for (int polls = 0;; ++polls) {
-    if (__atomic_load_n(host_word, __ATOMIC_ACQUIRE) >= value) return 1;
+    const uint64_t seen = __atomic_load_n(host_word, __ATOMIC_ACQUIRE);
+    if (seen & kFailed) return 2;
+    if (seen >= value) return 1;
     if (std::chrono::steady_clock::now() >= deadline) return 0;
     // a few quick polls, then sleep in steps of at most 200 us
     if (polls < 64) std::this_thread::yield();
@@ -190,26 +262,29 @@ int aegkv_fence_host_wait(const uint64_t* host_word, uint64_t value, int64_t tim
 }
 
 
-int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream) {
+int aegkv_fence_signal(uint64_t* word, uint64_t value, const uint64_t* guard,
+                       hipStream_t stream) {
   aegkv_clear_error();
-  int rc = check_word(word, "fence word");
+  int rc = check_value(value);
+  if (!rc) rc = check_word(word, "fence word");
+  if (!rc && guard) rc = check_word(guard, "move guard");
   if (rc) return rc;
   (void)hipGetLastError();  // clear a stale error: the check below is for this launch
-  hipLaunchKernelGGL(fence_signal_kernel, dim3(1), dim3(64), 0, stream, word, value);
+  hipLaunchKernelGGL(fence_signal_kernel, dim3(1), dim3(64), 0, stream, word, value, guard);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fence_signal_kernel launch");
   return 0;
 }
 
 int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
-                     uint64_t* timed_out, hipStream_t stream) {
+                     uint64_t* guard, hipStream_t stream) {
   aegkv_clear_error();
   if (timeout_us <= 0 || timeout_us > kMaxWaitMicros)
     return fail(AEGKV_ERANGE, "fence wait timeout %lld us outside (0, %lld]",
                 static_cast<long long>(timeout_us), static_cast<long long>(kMaxWaitMicros));
-  int rc = check_word(word, "fence word");
-  if (rc) return rc;
-  rc = check_word(timed_out, "timed_out flag");
+  int rc = check_value(value);
+  if (!rc) rc = check_word(word, "fence word");
+  if (!rc) rc = check_word(guard, "move guard");
   if (rc) return rc;
   int64_t khz = 0;
   rc = wall_clock_khz(&khz);
@@ -218,9 +293,21 @@ int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
   const uint64_t budget = static_cast<uint64_t>(timeout_us) * static_cast<uint64_t>(khz) / 1000u;
   (void)hipGetLastError();  // clear a stale error: the check below is for this launch
   hipLaunchKernelGGL(fence_wait_kernel, dim3(1), dim3(64), 0, stream, word, value, budget,
-                     timed_out);
+                     guard);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fence_wait_kernel launch");
+  return 0;
+}
+
+int aegkv_guard_merge(uint64_t* guard, const uint64_t* source_guard, hipStream_t stream) {
+  aegkv_clear_error();
+  int rc = check_word(guard, "move guard");
+  if (!rc) rc = check_word(source_guard, "source move guard");
+  if (rc) return rc;
+  (void)hipGetLastError();  // clear a stale error: the check below is for this launch
+  hipLaunchKernelGGL(guard_merge_kernel, dim3(1), dim3(64), 0, stream, guard, source_guard);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "guard_merge_kernel launch");
   return 0;
 }
 

@@ -24,6 +24,8 @@ from . import _lib
 MODE_AUTO = _lib.MODE_AUTO
 MODE_DIRECT = _lib.MODE_DIRECT
 MODE_STAGED = _lib.MODE_STAGED
+FENCE_FAILED = _lib.FENCE_FAILED
+MoveFailedError = _lib.MoveFailedError
 
 _MODES = {"auto": MODE_AUTO, "direct": MODE_DIRECT, "staged": MODE_STAGED}
 
@@ -141,6 +143,18 @@ def swap(
     _lib.check(rc)
 
 
+def _guard_ptr(words: torch.Tensor | None, index: int, what: str):
+    """Address of a move guard word (or None): a 1-D int64 tensor in pinned
+    host memory (GuardWords) or on the device."""
+    if words is None:
+        return None
+    if words.dtype != torch.int64 or words.dim() != 1 or not words.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous 1-D int64 tensor")
+    if not 0 <= index < words.numel():
+        raise ValueError(f"{what} index {index} outside [0, {words.numel()})")
+    return words.data_ptr() + 8 * index
+
+
 def _call_on(device: torch.device, fn):
     """Run fn() with `device` current, switching (and restoring) only when
     another device is current. Keeps no state, so threads may share it."""
@@ -204,8 +218,11 @@ class SegmentLayout:
 
     def swap(self, source_block_ids, target_block_ids, group_ids, first_kernel_blocks,
              valid_kernel_blocks, is_swap_in: bool, *, mode="auto",
-             stream: torch.cuda.Stream | None = None) -> None:
-        """One aegkv_swap_blocks call over this layout (see swap_segments)."""
+             stream: torch.cuda.Stream | None = None, guard: torch.Tensor | None = None,
+             guard_index: int = 0) -> None:
+        """One aegkv_swap_blocks call over this layout (see swap_segments).
+        guard (with guard_index): a move guard word (GuardWords.tensor); when
+        it is set by the time the stream reaches the swap, nothing moves."""
         src = _i64(source_block_ids)
         dst = _i64(target_block_ids)
         grp = _i32(group_ids)
@@ -217,10 +234,11 @@ class SegmentLayout:
                 f"source={src.size}, target={dst.size}, groups={grp.size}, "
                 f"first={first.size}, valid={valid.size}"
             )
+        gp = _guard_ptr(guard, guard_index, "guard")
         lib = _lib.load()
         rc = _call_on(self.device, lambda: lib.aegkv_swap_blocks(
             *self._args, src.size, _p64(src), _p64(dst), _p32(grp), _p64(first),
-            _p64(valid), 1 if is_swap_in else 0, _mode(mode),
+            _p64(valid), 1 if is_swap_in else 0, _mode(mode), gp,
             _stream_ptr(self.device, stream)))
         _lib.check(rc)
 
@@ -408,6 +426,8 @@ def migrate_blocks(
     *,
     segment_page_bytes: Sequence[int] | None = None,
     stream: torch.cuda.Stream | None = None,
+    guard: torch.Tensor | None = None,
+    guard_index: int = 0,
 ) -> None:
     """Whole-block copy from one cache to another of the same layout:
     dst_segments[s][dst[i]] := src_segments[s][src[i]] (aegkv_migrate_blocks).
@@ -419,6 +439,7 @@ def migrate_blocks(
     peer GPU's cache with peer access enabled; the work runs on the target
     cache's device. Each segment is viewed as [num_blocks, page] bytes; by
     default the page is the tensor's bytes / size(0), equal for both caches.
+    guard: a move guard word, as for SegmentLayout.swap.
     """
     if not src_segments or len(src_segments) != len(dst_segments):
         raise ValueError("one source and one target tensor per segment are required")
@@ -444,10 +465,11 @@ def migrate_blocks(
         raise ValueError("src and dst id lists differ in length")
     sb = (ctypes.c_void_p * len(src_segments))(*[t.data_ptr() for t in src_segments])
     db = (ctypes.c_void_p * len(dst_segments))(*[t.data_ptr() for t in dst_segments])
+    gp = _guard_ptr(guard, guard_index, "guard")
     lib = _lib.load()
     rc = _call_on(dev, lambda: lib.aegkv_migrate_blocks(
         len(dst_segments), sb, db, _p64(page), int(n_src), int(n_dst), src.size, _p64(src),
-        _p64(dst), _stream_ptr(dev, stream)))
+        _p64(dst), gp, _stream_ptr(dev, stream)))
     _lib.check(rc)
 
 
@@ -455,7 +477,9 @@ class _OwnedStream(torch.cuda.ExternalStream):
     """A torch stream over a HIP stream from aegkv_stream_create that
     destroys the HIP stream when the object goes (or on _aegkv_close()).
     weakref.finalize is not used: its callback was seen not to run for
-    torch stream objects."""
+    torch stream objects. Once closed, the stream's handle and its
+    synchronize / query / wait / record methods raise instead of handing
+    the runtime a destroyed stream."""
 
     def __init__(self, stream_ptr: int, device=None):
         self._aegkv_ptr = stream_ptr
@@ -463,7 +487,40 @@ class _OwnedStream(torch.cuda.ExternalStream):
     def _aegkv_close(self) -> None:
         ptr, self._aegkv_ptr = getattr(self, "_aegkv_ptr", None), None
         if ptr:
-            _lib.load().aegkv_stream_destroy(ctypes.c_void_p(ptr))
+            _lib.check(_lib.load().aegkv_stream_destroy(ctypes.c_void_p(ptr)))
+
+    def _aegkv_require_open(self) -> None:
+        if getattr(self, "_aegkv_ptr", None) is None:
+            raise RuntimeError("this dedicated stream is closed")
+
+    @property
+    def closed(self) -> bool:
+        return getattr(self, "_aegkv_ptr", None) is None
+
+    @property
+    def cuda_stream(self):
+        self._aegkv_require_open()
+        return super().cuda_stream
+
+    def synchronize(self):
+        self._aegkv_require_open()
+        return super().synchronize()
+
+    def query(self):
+        self._aegkv_require_open()
+        return super().query()
+
+    def wait_event(self, event):
+        self._aegkv_require_open()
+        return super().wait_event(event)
+
+    def wait_stream(self, stream):
+        self._aegkv_require_open()
+        return super().wait_stream(stream)
+
+    def record_event(self, event=None):
+        self._aegkv_require_open()
+        return super().record_event(event)
 
     def __del__(self, _finalizing=sys.is_finalizing):
         # At interpreter exit the HIP runtime may already be torn down, and
@@ -535,6 +592,16 @@ class DedicatedStream:
         self.stream._aegkv_close()
 
 
+def host_pinned_usage() -> tuple[int, int]:
+    """(pinned bytes the library holds, free bytes inside its uncached
+    blocks), from aegkv_host_usage: live cached pools plus every uncached
+    block kept, which is what counts against the host's cap on pinned
+    memory."""
+    pinned, free = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(_lib.load().aegkv_host_usage(ctypes.byref(pinned), ctypes.byref(free)))
+    return int(pinned.value), int(free.value)
+
+
 def _free_pinned(ptr: int) -> None:
     rc = _lib.load().aegkv_host_free(ptr)
     if rc:
@@ -555,18 +622,21 @@ class PinnedHostPool:
     uncached=True allocates from the uncached system pool
     (AEGKV_HOST_UNCACHED): faster swaps, especially both directions at
     once, but the library keeps such memory mapped until the process ends
-    and reuses it for later uncached pools of a fitting size.
+    and carves later uncached pools out of it. coherent=True allocates
+    fine-grained coherent memory (AEGKV_HOST_COHERENT), for words the GPU and
+    the host both write while kernels run (GuardWords).
     """
 
-    def __init__(self, nbytes: int, uncached: bool = False):
+    def __init__(self, nbytes: int, uncached: bool = False, coherent: bool = False):
         if nbytes <= 0:
             raise ValueError("pool size must be positive")
         lib = _lib.load()
         ptr = ctypes.c_void_p()
-        _lib.check(lib.aegkv_host_alloc_flags(ctypes.byref(ptr), int(nbytes),
-                                              _lib.HOST_UNCACHED if uncached else 0))
+        flags = (_lib.HOST_UNCACHED if uncached else 0) | (_lib.HOST_COHERENT if coherent else 0)
+        _lib.check(lib.aegkv_host_alloc_flags(ctypes.byref(ptr), int(nbytes), flags))
         self.nbytes = int(nbytes)
         self.uncached = uncached
+        self.coherent = coherent
         buf = (ctypes.c_uint8 * self.nbytes).from_address(ptr.value)
         fin = weakref.finalize(buf, _free_pinned, ptr.value)
         fin.atexit = False  # at interpreter exit the process releases it
@@ -575,6 +645,36 @@ class PinnedHostPool:
     def free(self) -> None:
         """Drop this pool's reference; the memory goes once no view remains."""
         self.tensor = None
+
+
+class GuardWords:
+    """Move guards: `num_words` uint64 words in coherent pinned host memory,
+    zeroed, that the GPU and the host both read and write (one per stream
+    that waits on fences; KVSwapper keeps one per swap stream).
+
+    A fence wait sets its stream's guard when it gives up (1) or when the
+    word it waits on carries the failure mark (2); guarded swaps and
+    migrations then move nothing, and guarded signals and publishes mark
+    the completion they report as failed (FENCE_FAILED), so every consumer
+    sees the failure. The library never clears a guard.
+    """
+
+    def __init__(self, num_words: int = 2):
+        if num_words <= 0:
+            raise ValueError("num_words must be positive")
+        self._pool = PinnedHostPool(8 * int(num_words), coherent=True)
+        self.tensor = self._pool.tensor.view(torch.int64)
+        self.tensor.zero_()
+        self.num_words = int(num_words)
+
+    def ptr(self, index: int) -> int:
+        return _guard_ptr(self.tensor, index, "guard")
+
+    def value(self, index: int) -> int:
+        """The guard as the host sees it now (0: not set)."""
+        if not 0 <= index < self.num_words:
+            raise ValueError(f"guard index {index} outside [0, {self.num_words})")
+        return int(self.tensor[index])
 
 
 def _fence_word(words: torch.Tensor, index: int, what: str) -> int:
@@ -587,51 +687,76 @@ def _fence_word(words: torch.Tensor, index: int, what: str) -> int:
     return words.data_ptr() + 8 * index
 
 
+def _fence_value(value: int) -> int:
+    if not 0 < value < FENCE_FAILED:
+        raise ValueError("fence values are positive and below 2**62 (bit 62 marks a failed move)")
+    return int(value)
+
+
 def fence_signal(words: torch.Tensor, index: int, value: int, *,
+                 guard: torch.Tensor | None = None, guard_index: int = 0,
                  stream: torch.cuda.Stream | None = None) -> None:
-    """Raise words[index] to at least `value` once every operation enqueued
-    earlier on `stream` (default: the current stream) has finished
+    """Raise words[index] to at least `value` once every operation
+    enqueued earlier on `stream` (default: the current stream) has finished
     (aegkv_fence_signal). The counterpart of recording an interprocess event
-    behind a swap (aegaeon/worker.py:2331,2349).
+    behind a swap (aegaeon/worker.py:2331,2349). With a move guard that is
+    set by then, the word is raised to value | FENCE_FAILED instead.
 
     words: a 1-D int64 tensor on the device, e.g. one shared with other
     processes through torch.multiprocessing (a HIP IPC memory handle).
     """
-    if not 0 < value < (1 << 63):
-        raise ValueError("fence values are positive and below 2**63")
+    value = _fence_value(value)
     ptr = _fence_word(words, index, "fence words")
+    gp = _guard_ptr(guard, guard_index, "guard")
     dev = words.device
     if dev.type != "cuda":
         raise ValueError("fence words must live on the device")
     lib = _lib.load()
-    rc = _call_on(dev, lambda: lib.aegkv_fence_signal(ptr, int(value), _stream_ptr(dev, stream)))
+    rc = _call_on(dev, lambda: lib.aegkv_fence_signal(ptr, value, gp, _stream_ptr(dev, stream)))
     _lib.check(rc)
 
 
-def fence_wait(words: torch.Tensor, index: int, value: int, timed_out: torch.Tensor,
-               timed_out_index: int = 0, *, timeout_s: float = 30.0,
+def fence_wait(words: torch.Tensor, index: int, value: int, guard: torch.Tensor,
+               guard_index: int = 0, *, timeout_s: float = 30.0,
                stream: torch.cuda.Stream | None = None) -> None:
     """Make every later operation on `stream` wait until words[index] >=
     value (aegkv_fence_wait); the counterpart of waiting on another worker's
     interprocess event (aegaeon/worker.py:2351-2394).
 
-    A wait that has polled for `timeout_s` seconds gives up, sets
-    timed_out[timed_out_index] to 1 and lets the stream go on; the flag is
-    never cleared here, so check it (after the stream has passed the wait)
-    before trusting what followed.
+    A wait that has polled for `timeout_s` seconds gives up and sets the
+    move guard guard[guard_index] to 1; a word that carries FENCE_FAILED
+    ends the wait at once and sets it to 2. The stream then goes on, but
+    guarded moves after the wait move nothing and guarded signals and
+    publishes report failure. guard: GuardWords.tensor, or a device int64
+    tensor on the words' device; the guard is never cleared here.
     """
-    if not 0 < value < (1 << 63):
-        raise ValueError("fence values are positive and below 2**63")
+    value = _fence_value(value)
     ptr = _fence_word(words, index, "fence words")
-    flag = _fence_word(timed_out, timed_out_index, "timed_out")
+    gp = _guard_ptr(guard, guard_index, "guard")
     dev = words.device
-    if dev.type != "cuda" or timed_out.device != dev:
-        raise ValueError("fence words and the timed_out flags must live on one device")
+    if dev.type != "cuda":
+        raise ValueError("fence words must live on the device")
+    if guard.device.type == "cuda" and guard.device != dev:
+        raise ValueError("fence words and a device guard must live on one device")
     timeout_us = int(timeout_s * 1e6)
     lib = _lib.load()
-    rc = _call_on(dev, lambda: lib.aegkv_fence_wait(ptr, int(value), timeout_us, flag,
+    rc = _call_on(dev, lambda: lib.aegkv_fence_wait(ptr, value, timeout_us, gp,
                                                     _stream_ptr(dev, stream)))
     _lib.check(rc)
+
+
+def guard_merge(guard: torch.Tensor, index: int, source: torch.Tensor, source_index: int, *,
+                device: torch.device | None = None,
+                stream: torch.cuda.Stream | None = None) -> None:
+    """Once `stream` (default: the current stream of `device`) reaches it, set
+    guard[index] to 2 (a source failed) when source[source_index] is set
+    (aegkv_guard_merge): a consumer that waits on a producer's completion
+    event inherits the producer's failure."""
+    gp = _guard_ptr(guard, index, "guard")
+    sp = _guard_ptr(source, source_index, "source guard")
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    lib = _lib.load()
+    _lib.check(_call_on(dev, lambda: lib.aegkv_guard_merge(gp, sp, _stream_ptr(dev, stream))))
 
 
 class HostFenceWords:
@@ -643,6 +768,8 @@ class HostFenceWords:
 
     HostFenceWords(n) creates a new zeroed file (its `name` is the path) and
     removes it on close(); HostFenceWords.attach(name) maps an existing one.
+    close() first waits for every stream that a publish into these words was
+    enqueued on, so no host function writes into an unmapped page.
     """
 
     def __init__(self, num_words: int | None = None, *, _name: str | None = None):
@@ -682,6 +809,9 @@ class HostFenceWords:
         self._anchor = ctypes.c_char.from_buffer(self._mm)
         self._base = ctypes.addressof(self._anchor)
         self.words = np.frombuffer(self._mm, dtype=np.uint64)
+        # streams holding publishes into these words: stream handle -> stream
+        self._publishers: dict = {}
+        self._publishers_lock = threading.Lock()
 
     @classmethod
     def attach(cls, name: str) -> "HostFenceWords":
@@ -694,13 +824,23 @@ class HostFenceWords:
             raise ValueError(f"host fence index {index} outside [0, {self.num_words})")
         return self._base + 8 * index
 
+    def _note_publisher(self, stream: torch.cuda.Stream) -> None:
+        with self._publishers_lock:
+            self._publishers[stream.cuda_stream] = stream
+
     def close(self) -> None:
-        """Unmap (and remove the file, for the creator). Callers first make
-        sure no stream still holds a publish into these words."""
+        """Wait for the streams that publishes into these words were enqueued
+        on (a closed dedicated stream was synchronized when it closed), then
+        unmap, and remove the file for the creator."""
         import os
 
         if self._mm is None:
             return
+        with self._publishers_lock:
+            streams, self._publishers = list(self._publishers.values()), {}
+        for st in streams:
+            if not getattr(st, "closed", False):
+                st.synchronize()
         self.words = None
         self._anchor = None
         self._mm.close()
@@ -728,30 +868,41 @@ def attached_host_fence_words(name: str) -> HostFenceWords:
 
 
 def fence_publish(host_words: HostFenceWords, index: int, value: int, *,
+                  guard: torch.Tensor | None = None, guard_index: int = 0,
                   device: torch.device | None = None,
                   stream: torch.cuda.Stream | None = None) -> None:
     """Raise host_words[index] to at least `value` once every operation
     enqueued earlier on `stream` (default: the current stream of `device`)
-    has finished (aegkv_fence_publish, a host function on the stream)."""
-    if not 0 < value < (1 << 63):
-        raise ValueError("fence values are positive and below 2**63")
+    has finished (aegkv_fence_publish, a host function on the stream). With
+    a move guard (GuardWords.tensor: the host function reads it) that is set
+    by then, the word is raised to value | FENCE_FAILED instead."""
+    value = _fence_value(value)
     ptr = host_words.ptr(index)
+    gp = _guard_ptr(guard, guard_index, "guard")
+    if guard is not None and guard.device.type != "cpu":
+        raise ValueError("a published fence's guard must be pinned host memory (GuardWords)")
     dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    st = stream if stream is not None else torch.cuda.current_stream(dev)
     lib = _lib.load()
-    rc = _call_on(dev, lambda: lib.aegkv_fence_publish(ptr, int(value), _stream_ptr(dev, stream)))
+    rc = _call_on(dev, lambda: lib.aegkv_fence_publish(ptr, value, gp, st.cuda_stream))
     _lib.check(rc)
+    host_words._note_publisher(st)
 
 
 def fence_host_wait(host_words: HostFenceWords, index: int, value: int,
                     timeout_s: float = 0.0) -> bool:
     """True once host_words[index] >= value; waits on this thread for at most
-    timeout_s seconds (0: look once). No GPU call; the GIL is released."""
-    if not 0 < value < (1 << 63):
-        raise ValueError("fence values are positive and below 2**63")
+    timeout_s seconds (0: look once). No GPU call; the GIL is released.
+    Raises MoveFailedError when the word carries the failure mark."""
+    value = _fence_value(value)
     if timeout_s < 0:
         raise ValueError("timeout_s must be >= 0")
-    rc = _lib.load().aegkv_fence_host_wait(host_words.ptr(index), int(value),
+    rc = _lib.load().aegkv_fence_host_wait(host_words.ptr(index), value,
                                            int(timeout_s * 1e6))
     if rc < 0:
         _lib.check(rc)
+    if rc == 2:
+        raise MoveFailedError(f"host fence {host_words.name}[{index}] carries the failure mark: "
+                              f"the move it counts (value {value}) or one before it on its "
+                              "stream moved nothing")
     return rc == 1

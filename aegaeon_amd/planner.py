@@ -204,10 +204,16 @@ class BlockPools:
         (block_manager.py:1498-1518).
 
         events: one completion event per worker that runs the move (objects
-        with query() -> bool and synchronize(), e.g. the torch.cuda.Event
-        KVSwapper.swap_blocks returns). finished: optional predicate that is
-        true once every request of the move has finished, after which the
-        move counts as done without looking at its events.
+        with query() -> bool and synchronize(), e.g. the MoveEvent
+        KVSwapper.swap_blocks returns or a FenceToken). finished: optional
+        predicate that is true once every request of the move has finished,
+        after which the move counts as done without looking at its events.
+
+        An event whose move failed (a fence wait before it gave up, or a move
+        it waited for failed) raises MoveFailedError from query() and
+        synchronize(): the reclaim calls let it through and leave the move in
+        the ledger, so its source ids are never freed for a move that did not
+        happen (the reference stops the worker, worker.py:2364-2368).
         """
         rec = MoveRecord(next(self._serial), plan, list(events), finished)
         n = len(plan.release_source_block_ids)

@@ -24,13 +24,25 @@ word has reached the count. With fence_host (host fence words in a shared
 swap, so a controller in any process can poll the token on the CPU
 (FenceToken.query / synchronize) before it frees the move's source blocks.
 Ray object refs are not part of this module.
+
+Failed waits. The reference waits on source events without a limit
+(worker.py:2387) and stops the worker when it cannot get them
+(:2364-2368), so a swap never reads a block before its producer wrote it.
+Here a fence wait is bounded, and a wait that gives up sets the swap
+stream's move guard (ops.GuardWords, one word per swap stream). Every swap
+on that stream then moves nothing, its fence signal and host publish carry
+the failure mark (ops.FENCE_FAILED), consumers of its MoveEvent or
+FenceToken get MoveFailedError instead of completion, and a consumer's own
+guard inherits the failure (through the fence word, or ops.guard_merge
+behind a producer's event). A failure is sticky, like the reference's
+stopped worker: the stream's later swaps fail too.
 """
 
 from __future__ import annotations
 
 import logging
 import weakref
-from collections import defaultdict
+from collections import defaultdict, deque
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Sequence, Tuple, Union
 
@@ -69,45 +81,103 @@ class FenceToken:
         return ops.attached_host_fence_words(self.host)
 
     def query(self) -> bool:
-        """True once the swap behind this token has finished."""
+        """True once the swap behind this token has finished; MoveFailedError
+        if it (or an earlier swap on its stream) failed and moved nothing."""
         return ops.fence_host_wait(self._host_words(), self.slot, self.value, 0.0)
 
     def synchronize(self, timeout_s: float = 600.0) -> None:
         """Block this thread until the swap has finished; TimeoutError after
-        timeout_s seconds."""
+        timeout_s seconds, MoveFailedError if it failed."""
         if not ops.fence_host_wait(self._host_words(), self.slot, self.value, timeout_s):
             raise TimeoutError(f"fence {self.slot} did not reach {self.value} within "
                                f"{timeout_s} s")
 
 
+class MoveEvent(torch.cuda.Event):
+    """Completion event of one swap or migration (what KVSwapper.swap_blocks
+    and migrate_blocks return): a torch.cuda.Event recorded behind the move
+    that also knows the move guard of the stream it ran on. query() and
+    synchronize() raise MoveFailedError once the move has completed with
+    that guard set (a fence wait before it gave up, or a move it waited for
+    had failed: it moved nothing), so a ledger never frees the sources of a
+    move that did not happen. The guard is the stream's, so a failure there
+    also fails the stream's earlier events that are looked at afterwards.
+    Swappers that list it as a source event inherit the failure through
+    ops.guard_merge."""
+
+    def __new__(cls, guards: "ops.GuardWords", side: int, interprocess: bool = False):
+        return super().__new__(cls, interprocess=interprocess)
+
+    def __init__(self, guards: "ops.GuardWords", side: int, interprocess: bool = False):
+        self.guards = guards
+        self.side = side
+
+    @property
+    def failed(self) -> bool:
+        """True when the stream's guard is set (meaningful once complete)."""
+        return self.guards.value(self.side) != 0
+
+    def _raise_if_failed(self) -> None:
+        why = self.guards.value(self.side)
+        if why:
+            direction = "in" if self.side else "out"
+            cause = "a fence wait timed out" if why == 1 else "a source move failed"
+            raise ops.MoveFailedError(
+                f"the move behind this event ran on a swap-{direction} stream whose guard is "
+                f"set ({cause}): it moved nothing")
+
+    def query(self) -> bool:
+        done = super().query()
+        if done:
+            self._raise_if_failed()
+        return done
+
+    def synchronize(self) -> None:
+        super().synchronize()
+        self._raise_if_failed()
+
+
 _ipc_event_refusal: Dict[int, Optional[str]] = {}
 
 # Fences raised by swappers of this process: (address of the fence words,
-# slot) -> (count, completion event of the swap that raised it, the raising
-# swapper). A waiting fence kernel holds its stream's hardware queue, and a
-# stream of this process may share that queue with the producing stream, so
-# a token produced here is waited on through the producer's event instead.
-# An entry holds only while its swapper lives: the swapper keeps its fence
-# words alive, and once both are gone the address may belong to other words.
-_local_fences: Dict[Tuple[int, int], Tuple[int, torch.cuda.Event, "weakref.ref"]] = {}
+# slot) -> (the raising swapper, its recent (count, completion event) pairs
+# in count order). A waiting fence kernel holds its stream's hardware queue,
+# and a stream of this process may share that queue with the producing
+# stream, so a token produced here is waited on through the producer's
+# event instead: the event of the smallest recorded count that reaches the
+# token's value, so a consumer waits for the move it names and not for later
+# ones queued behind it. An entry holds only while its swapper lives: the
+# swapper keeps its fence words alive, and once both are gone the address
+# may belong to other words.
+_LOCAL_FENCE_HISTORY = 64
+_local_fences: Dict[Tuple[int, int], Tuple["weakref.ref", deque]] = {}
 
 
 def _note_local_fence(words_ptr: int, slot: int, count: int, event, owner) -> None:
-    _local_fences[(words_ptr, slot)] = (count, event, weakref.ref(owner))
+    entry = _local_fences.get((words_ptr, slot))
+    if entry is None or entry[0]() is not owner:
+        entry = (weakref.ref(owner), deque(maxlen=_LOCAL_FENCE_HISTORY))
+        _local_fences[(words_ptr, slot)] = entry
+    entry[1].append((count, event))
 
 
 def _local_fence_event(words_ptr: int, slot: int, value: int):
-    """The event of this process's swap that raised (words, slot) to at
-    least `value`, or None (not raised here, not that far yet, or raised by
-    a swapper that no longer exists)."""
+    """The completion event of this process's swap that raised (words, slot)
+    to `value` (the first recorded count >= value; once the history no
+    longer holds that count, the oldest one kept, which completes after it),
+    or None (not raised here, not that far yet, or raised by a swapper that
+    no longer exists)."""
     entry = _local_fences.get((words_ptr, slot))
     if entry is None:
         return None
-    count, event, owner = entry
+    owner, history = entry
     if owner() is None:
         del _local_fences[(words_ptr, slot)]
         return None
-    return event if count >= value else None
+    for count, event in history:
+        if count >= value:
+            return event
+    return None
 
 
 def interprocess_event_refusal(device: torch.device) -> Optional[str]:
@@ -254,7 +324,9 @@ class KVSwapper:
         self.fence_slots = tuple(fence_slots) if fence_slots is not None else None
         self.fence_timeout_s = fence_timeout_s
         self._fence_count = [0, 0]
-        self._fence_timed_out = torch.zeros(2, dtype=torch.int64, device=device)
+        # move guards of the swap-out (0) and swap-in (1) streams, set by a
+        # failed fence wait or inherited from a failed source move
+        self.guards = ops.GuardWords(2)
         self.last_fence: Optional[FenceToken] = None
         # other engines' caches this worker can migrate blocks from
         self._own_pages = [cache.segment_pages(i) for i in range(len(cache.segments))]
@@ -287,16 +359,19 @@ class KVSwapper:
         groups = np.asarray(group_ids, dtype=np.int64).reshape(-1)
         if groups.size and (groups.min() < 0 or groups.max() >= len(self.group_descriptors)):
             bad = groups[(groups < 0) | (groups >= len(self.group_descriptors))][0]
-            raise ValueError(f"Invalid swap cache-group id {int(bad)}")
+            raise ValueError(f"cache-group id {int(bad)} of a swap entry is not one of the "
+                             f"{len(self.group_descriptors)} groups")
+        side = 1 if is_swap_in else 0
+        self._require_not_failed(side)
         stream = self.swap_in_stream if is_swap_in else self.swap_out_stream
-        new_event = torch.cuda.Event(interprocess=self.interprocess_events)
+        new_event = MoveEvent(self.guards, side, interprocess=self.interprocess_events)
         # wait for in-flight moves of the same requests (worker.py:2351-2394);
         # bytes are IPC handles exported by another process
-        side = 1 if is_swap_in else 0
         self._wait_sources(request_ids, source_events, stream, side)
         self._layout.swap(source_block_ids, target_block_ids, groups.astype(np.int32),
                           first_kernel_blocks, valid_kernel_blocks, is_swap_in,
-                          mode=self.mode if mode is None else mode, stream=stream)
+                          mode=self.mode if mode is None else mode, stream=stream,
+                          guard=self.guards.tensor, guard_index=side)
         self._finish(request_ids, side, stream, new_event)
         if logger.isEnabledFor(logging.INFO):
             valid = np.asarray(valid_kernel_blocks, dtype=np.int64).reshape(-1)
@@ -312,26 +387,47 @@ class KVSwapper:
 
     def _wait_sources(self, request_ids, source_events, stream, side: int) -> None:
         """Order `stream` after the requests' previous moves
-        (worker.py:2351-2394): local events, IPC event handles or fences."""
+        (worker.py:2351-2394): local events, IPC event handles or fences.
+        A source move's failure reaches this stream's guard: through the
+        fence word for a FenceToken from another process, through
+        ops.guard_merge for a MoveEvent or a token raised in this process.
+        Each distinct source is waited on once."""
         if len(source_events) != len(request_ids):
             raise ValueError("one source event slot per request is required")
+        seen_events, seen_tokens, merged = set(), set(), set()
+
+        def merge_from(ev) -> None:
+            if isinstance(ev, MoveEvent) and (id(ev.guards), ev.side) not in merged:
+                merged.add((id(ev.guards), ev.side))
+                ops.guard_merge(self.guards.tensor, side, ev.guards.tensor, ev.side,
+                                device=self.device, stream=stream)
+
         for ev in source_events:
-            if ev is not None:
-                if isinstance(ev, FenceToken):
-                    if self.fence_words is None:
-                        raise ValueError("a FenceToken source needs fence_words")
-                    local = _local_fence_event(self.fence_words.data_ptr(), ev.slot, ev.value)
-                    if local is not None:
-                        # raised in this process: the swap that raised it this
-                        # far follows the one the token names on its stream
-                        stream.wait_event(local)
-                        continue
-                    ops.fence_wait(self.fence_words, ev.slot, ev.value, self._fence_timed_out,
-                                   side, timeout_s=self.fence_timeout_s, stream=stream)
-                else:
-                    if isinstance(ev, (bytes, bytearray)):
-                        ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
-                    stream.wait_event(ev)
+            if ev is None:
+                continue
+            if isinstance(ev, FenceToken):
+                if (ev.slot, ev.value) in seen_tokens:
+                    continue
+                seen_tokens.add((ev.slot, ev.value))
+                if self.fence_words is None:
+                    raise ValueError("a FenceToken source needs fence_words")
+                local = _local_fence_event(self.fence_words.data_ptr(), ev.slot, ev.value)
+                if local is not None:
+                    # raised in this process: wait on the producer's event
+                    # and take over its stream's failure, if any
+                    stream.wait_event(local)
+                    merge_from(local)
+                    continue
+                ops.fence_wait(self.fence_words, ev.slot, ev.value, self.guards.tensor, side,
+                               timeout_s=self.fence_timeout_s, stream=stream)
+            else:
+                if id(ev) in seen_events:
+                    continue
+                seen_events.add(id(ev))
+                if isinstance(ev, (bytes, bytearray)):
+                    ev = torch.cuda.Event.from_ipc_handle(self.device, bytes(ev))
+                stream.wait_event(ev)
+                merge_from(ev)
 
     def _finish(self, request_ids, side: int, stream, new_event: torch.cuda.Event) -> None:
         """Record the move's completion event behind the enqueued work, list
@@ -346,12 +442,13 @@ class KVSwapper:
         if self.fence_slots is not None:
             self._fence_count[side] += 1
             slot, count = self.fence_slots[side], self._fence_count[side]
-            ops.fence_signal(self.fence_words, slot, count, stream=stream)
+            ops.fence_signal(self.fence_words, slot, count, guard=self.guards.tensor,
+                             guard_index=side, stream=stream)
             _note_local_fence(self.fence_words.data_ptr(), slot, count, event, self)
             host = None
             if self.fence_host is not None:
-                ops.fence_publish(self.fence_host, slot, count, device=self.device,
-                                  stream=stream)
+                ops.fence_publish(self.fence_host, slot, count, guard=self.guards.tensor,
+                                  guard_index=side, device=self.device, stream=stream)
                 host = self.fence_host.name
             self.last_fence = FenceToken(slot, count, host)
 
@@ -396,11 +493,13 @@ class KVSwapper:
             raise KeyError(f"engine {source_engine_id}'s cache is not registered")
         if len(source_block_ids) != len(target_block_ids):
             raise ValueError("source and target block lists differ in length")
+        self._require_not_failed(1)
         stream = self.swap_in_stream
-        new_event = torch.cuda.Event(interprocess=self.interprocess_events)
+        new_event = MoveEvent(self.guards, 1, interprocess=self.interprocess_events)
         self._wait_sources(request_ids, source_events, stream, 1)
         ops.migrate_blocks(self.peer_caches[source_engine_id], self._own_pages,
-                           source_block_ids, target_block_ids, stream=stream)
+                           source_block_ids, target_block_ids, stream=stream,
+                           guard=self.guards.tensor, guard_index=1)
         self._finish(request_ids, 1, stream, new_event)
         return new_event
 
@@ -417,14 +516,18 @@ class KVSwapper:
         for rid in request_ids:
             self.clear_request_resource(rid)
 
-    def _check_fences(self, side: int, stream: torch.cuda.Stream) -> None:
-        with torch.cuda.stream(stream):
-            if int(self._fence_timed_out[side].item()):
-                self._fence_timed_out[side].zero_()
-                raise RuntimeError(
-                    f"a swap-{'in' if side else 'out'} waited {self.fence_timeout_s} s for a "
-                    "source fence that was never signalled; swaps after that wait may have "
-                    "read data before its producer wrote it")
+    def _require_not_failed(self, side: int) -> None:
+        """MoveFailedError once this side's guard is set (as the host sees it
+        now; the device also stops every later guarded swap on the stream)."""
+        why = self.guards.value(side)
+        if why:
+            direction = "in" if side else "out"
+            cause = (f"a fence wait gave up after {self.fence_timeout_s} s" if why == 1
+                     else "a move it waited for had failed")
+            raise ops.MoveFailedError(
+                f"this swapper's swap-{direction} stream has failed ({cause}): its swaps from "
+                "then on moved nothing and their completion reports failure; the failure is "
+                "sticky, as the reference stops the worker")
 
     def _require_open(self) -> None:
         if self.swap_in_stream is None:
@@ -443,11 +546,15 @@ class KVSwapper:
         self.swap_in_stream = self.swap_out_stream = None
 
     def wait_for_all_move_in(self) -> None:
+        """Wait for every swap-in (worker.py:2406-2412); MoveFailedError if the
+        swap-in stream's guard is set."""
         self._require_open()
         self.swap_in_stream.synchronize()
-        self._check_fences(1, self.swap_in_stream)
+        self._require_not_failed(1)
 
     def wait_for_all_move_out(self) -> None:
+        """Wait for every swap-out (worker.py:2414-2418); MoveFailedError if the
+        swap-out stream's guard is set."""
         self._require_open()
         self.swap_out_stream.synchronize()
-        self._check_fences(0, self.swap_out_stream)
+        self._require_not_failed(0)

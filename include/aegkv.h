@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define AEGKV_ABI_VERSION 2
+#define AEGKV_ABI_VERSION 3
 
 /* status codes (negative: rejected before any work was enqueued) */
 #define AEGKV_OK 0
@@ -110,6 +110,16 @@ extern "C" {
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);
 
+/*
+ * Set-up, once per process, before the first call (optional, but needed
+ * before any call made under stream capture): for every visible device,
+ * with that device current, looks up the device array the allocation-free
+ * copy uses (which may load the library's code object) and the device's CU
+ * count, then restores the current device. Returns 0 when there is no
+ * device. No counterpart in the reference.
+ */
+int aegkv_init(void);
+
 /* Message for the calling thread's most recent failure ("" if none). */
 const char* aegkv_last_error(void);
 
@@ -134,6 +144,25 @@ int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
                int64_t block_bytes, int mode, hipStream_t stream);
 
 /*
+ * Move guards. A guard is an 8-byte aligned uint64 in mapped pinned host
+ * memory (aegkv_host_alloc_flags with AEGKV_HOST_COHERENT) or device
+ * memory, owned by the caller, one per stream that waits on fences.
+ * aegkv_fence_wait sets it when the wait gives up (1) or when the awaited
+ * word carries AEGKV_FENCE_FAILED (2); aegkv_guard_merge sets it to 2 when
+ * another guard is set. The library never clears a guard. Calls that take a guard
+ * read it when the stream reaches them: a guarded swap or migration then
+ * moves nothing, a guarded signal or publish raises its word to
+ * value | AEGKV_FENCE_FAILED. So once a wait has failed, no later move on
+ * that stream reads its source and every consumer of its completion sees
+ * the failure, as the reference never runs a swap before its source
+ * (aegaeon/worker.py:2387) and stops the worker when the source events
+ * cannot be had (:2364-2368). A STAGED swap-out that a set guard skips
+ * leaves its target host pages undefined (the runtime's copies from
+ * staging still run); DIRECT and swap-ins write nothing.
+ */
+#define AEGKV_FENCE_FAILED (1ull << 62)
+
+/*
  * Segmented (composite-page) swap. Replaces the data-plane loop of
  * Worker.swap_blocks, aegaeon/worker.py:2265-2329, whose layout comes from
  * aegaeon/vllm_cache.py:75-101 and aegaeon/worker.py:1419-1432.
@@ -156,6 +185,8 @@ int aegkv_swap(const int64_t* source_block_ids, const int64_t* target_block_ids,
  *   is_swap_in: dev[0,len) <- host[0,len)  (host_id = source, dev_id = target)
  *   otherwise:  host[0,len) <- dev[0,len)  (dev_id = source, host_id = target)
  * Entries with len == 0 and segments not owned by g move nothing.
+ * guard: null, or a move guard (see above); when it is set by the time the
+ * stream reaches the call, nothing moves.
  */
 int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
                       const int64_t* segment_page_bytes,
@@ -172,7 +203,7 @@ int aegkv_swap_blocks(int32_t num_segments, void* const* segment_bases,
                       const int32_t* group_ids,
                       const int64_t* first_kernel_blocks,
                       const int64_t* valid_kernel_blocks,
-                      int is_swap_in, int mode, hipStream_t stream);
+                      int is_swap_in, int mode, const uint64_t* guard, hipStream_t stream);
 
 /*
  * In-HBM block copy / compaction: for every segment s and pair i,
@@ -250,13 +281,14 @@ int aegkv_copy_probe(int kind, int32_t num_segments, void* const* segment_bases,
  * GPU's memory over xGMI once peer access is enabled. Targets must be
  * distinct (AEGKV_EDUP); the two caches must not overlap (AEGKV_EOVERLAP;
  * use aegkv_copy_blocks within one cache). Same kernel and launch shape as
- * aegkv_copy_blocks.
+ * aegkv_copy_blocks. guard: null, or a move guard; when it is set by the
+ * time the stream reaches the call, nothing moves.
  */
 int aegkv_migrate_blocks(int32_t num_segments, void* const* src_segment_bases,
                          void* const* dst_segment_bases, const int64_t* segment_page_bytes,
                          int64_t src_num_blocks, int64_t dst_num_blocks, int64_t num_pairs,
                          const int64_t* src_block_ids, const int64_t* dst_block_ids,
-                         hipStream_t stream);
+                         const uint64_t* guard, hipStream_t stream);
 
 /*
  * Weight load on a model switch: num_slices contiguous slices, pinned host
@@ -312,10 +344,18 @@ int aegkv_transfer_entries(int32_t num_groups, const int32_t* group_kind,
  * can lose their overlap; a stream created with a CU mask gets a queue to
  * itself (the mask here enables every CU). Default priority. It is a
  * blocking stream: it synchronizes with the legacy default (null) stream.
- * aegkv_stream_destroy waits for the stream's queued work, then destroys it.
+ * aegkv_stream_destroy waits for the stream's queued work, drops every event
+ * the library recorded on it, then destroys it.
+ *
+ * aegkv_stream_release(stream): wait for the stream's queued work and drop
+ * every event the library recorded on it (descriptor-ring and STAGED fork
+ * events). Call it before destroying, by any other means, a stream that
+ * library calls ran on; the library then never queries, waits on or
+ * re-records an event whose stream is gone. The stream stays usable.
  */
 int aegkv_stream_create(hipStream_t* stream);
 int aegkv_stream_destroy(hipStream_t stream);
+int aegkv_stream_release(hipStream_t stream);
 
 /*
  * The same, on a subset of the CUs: bit i of cu_mask (mask_words 32-bit
@@ -344,18 +384,31 @@ int aegkv_host_alloc(void** ptr, int64_t bytes);
  * (hipHostMallocUncached): kernel loads and stores to it bypass the GPU L2.
  * Measured on MI355X with the swap kernels: swap-out 56.6 -> 57.0 GB/s,
  * both directions at once 87 -> 90 GB/s; a blit hipMemcpyAsync is
- * unchanged. Such a pool is never returned to the runtime before the
- * process ends: aegkv_host_free parks it, and a later uncached allocation
- * that it fits reuses it (the smallest such parked pool), which keeps a
- * process whose pools come and go under the host's cap on pinned memory.
- * Meant for long-lived pools such as a KV host pool.
+ * unchanged. Uncached memory is never returned to the runtime before the
+ * process ends: uncached pools are carved out of uncached blocks the
+ * library keeps, aegkv_host_free returns a pool's range to a free list
+ * (merged with free neighbours), and a later uncached pool takes the
+ * smallest free range that fits before a new block is allocated. A process
+ * whose pools come and go in different sizes therefore pins no more than
+ * its largest set of live pools at once, which keeps it under the host's
+ * cap on pinned memory. Meant for long-lived pools such as a KV host pool.
+ * AEGKV_HOST_COHERENT allocates fine-grained coherent memory
+ * (hipHostMallocCoherent), for words both the GPU and the host write and
+ * read while kernels run, such as move guards.
  */
 #define AEGKV_HOST_UNCACHED 1
+#define AEGKV_HOST_COHERENT 2
 int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags);
 /* Release a pool from aegkv_host_alloc(_flags); null is a no-op, any other
  * pointer that is not a live pool (freed twice, or not from this library)
  * is rejected with AEGKV_EINVAL. */
 int aegkv_host_free(void* ptr);
+
+/* Pinned memory this library holds, for callers that budget against the
+ * host's cap: *pinned_bytes = live cached pools + every uncached block kept
+ * (live or free), *uncached_free_bytes = the free part of those blocks.
+ * Either pointer may be null. Host-only. No counterpart in the reference. */
+int aegkv_host_usage(int64_t* pinned_bytes, int64_t* uncached_free_bytes);
 
 /*
  * Fences: ordering a stream after work enqueued on another stream, in this
@@ -372,24 +425,37 @@ int aegkv_host_free(void* ptr);
  *
  * aegkv_fence_signal: once every operation enqueued on `stream` before it
  * has finished, raise *word to at least `value` (atomic max, release at
- * system scope). Give each producing stream its own word and signal
- * increasing values.
+ * system scope; 0 < value < 2^62). Give each producing stream its own word
+ * and signal increasing values. With a guard (may be null) that is set by
+ * then, the word is raised to value | AEGKV_FENCE_FAILED instead.
  *
  * aegkv_fence_wait: every operation enqueued on `stream` after this call
  * runs after *word has reached `value` (acquire at system scope). The wait
  * gives up after `timeout_us` microseconds (0 < timeout_us <= 600 s) of
- * polling; it then stores 1 into *timed_out and lets the stream continue, so
- * the caller must check *timed_out (it is never cleared by the library)
- * before trusting what the stream produced after the wait. A waiting fence
+ * polling and then sets the move guard *guard to 1; a word that carries
+ * AEGKV_FENCE_FAILED ends the wait at once and sets *guard to 2. Either way
+ * the stream continues, and guarded calls after the wait move nothing and
+ * mark their completion failed (see "Move guards"). A waiting fence
  * holds its stream's hardware queue: the signal it waits for must come from
  * another process or from a stream on a hardware queue of its own
  * (aegkv_stream_create), never from a stream that may share the waiting
  * stream's queue (plain streams share the process's few queues), or it
  * runs only after the wait has timed out.
  */
-int aegkv_fence_signal(uint64_t* word, uint64_t value, hipStream_t stream);
+int aegkv_fence_signal(uint64_t* word, uint64_t value, const uint64_t* guard,
+                       hipStream_t stream);
 int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
-                     uint64_t* timed_out, hipStream_t stream);
+                     uint64_t* guard, hipStream_t stream);
+
+/*
+ * Once the stream reaches it, set *guard to 2 (a source failed) when
+ * *source_guard is non-zero (one single-lane kernel). For a consumer that orders its
+ * stream after a producer's completion event rather than a fence word: the
+ * producer's failure then stops the consumer's guarded moves too. Both are
+ * move guards. No counterpart in the reference (its event waits carry no
+ * failure).
+ */
+int aegkv_guard_merge(uint64_t* guard, const uint64_t* source_guard, hipStream_t stream);
 
 /*
  * Host-side fence completion, for a controller that polls moves on the CPU
@@ -402,17 +468,22 @@ int aegkv_fence_wait(const uint64_t* word, uint64_t value, int64_t timeout_us,
  * by other processes it lives in a mapping they share (a /dev/shm file).
  *
  * aegkv_fence_publish: once every operation enqueued on `stream` before it
- * has finished, raise *host_word to at least `value` (0 < value < 2^63;
+ * has finished, raise *host_word to at least `value` (0 < value < 2^62;
  * atomic max, release). It is a host function on the stream (hipLaunchHostFunc):
  * the stream is held by the runtime, no wave waits on a CU. The mapping must
- * stay valid until the stream has passed it.
+ * stay valid until the stream has passed it. With a guard (null, or a move
+ * guard in pinned host memory, which the host function reads) that is set
+ * by then, the word is raised to value | AEGKV_FENCE_FAILED instead.
  *
  * aegkv_fence_host_wait: on the calling thread, wait until *host_word >=
  * value (acquire), for at most timeout_us microseconds (0: look once;
- * at most 600 s). Returns 1 once reached, 0 if not within the time, a
- * negative status on a bad argument. No HIP call.
+ * at most 600 s). Returns 1 once reached, 2 as soon as the word carries
+ * AEGKV_FENCE_FAILED (the move, or one before it on the same stream,
+ * failed), 0 if neither within the time, a negative status on a bad
+ * argument. No HIP call.
  */
-int aegkv_fence_publish(uint64_t* host_word, uint64_t value, hipStream_t stream);
+int aegkv_fence_publish(uint64_t* host_word, uint64_t value, const uint64_t* guard,
+                        hipStream_t stream);
 int aegkv_fence_host_wait(const uint64_t* host_word, uint64_t value, int64_t timeout_us);
 
 #ifdef __cplusplus

@@ -7,7 +7,9 @@
  *   2. aegkv_swap_blocks swap-in of those pages to 10 other device blocks,
  *   3. aegkv_copy_blocks of 8 pairs,
  *   4. a rejected call (a target id out of range): negative status, a
- *      message, and nothing changed.
+ *      message, and nothing changed,
+ *   5. a swap-in behind a set move guard: nothing moves.
+ * The swap-in of step 2 runs with a clear guard (a coherent pinned word).
  * `abi_check --version` only prints the library's ABI version (no GPU).
  * Exit status 0 and the last line "c-abi ok" on success.
  */
@@ -62,6 +64,10 @@ int main(int argc, char** argv) {
     return aegkv_abi_version() == AEGKV_ABI_VERSION ? 0 : 1;
   }
   HIPCHK(hipSetDevice(0));
+  if (aegkv_init() != 0) {
+    fprintf(stderr, "aegkv_init: %s\n", aegkv_last_error());
+    return 2;
+  }
   hipStream_t stream;
   HIPCHK(hipStreamCreate(&stream));
 
@@ -89,6 +95,13 @@ int main(int argc, char** argv) {
   memset(host, 0, (size_t)(NHOST * composite));
   unsigned char* want_host = calloc((size_t)(NHOST * composite), 1);
   if (!want_host) return 2;
+  uint64_t* guard = NULL;
+  rc = aegkv_host_alloc_flags((void**)&guard, 64, AEGKV_HOST_COHERENT);
+  if (rc) {
+    fprintf(stderr, "aegkv_host_alloc_flags(coherent): %d %s\n", rc, aegkv_last_error());
+    return 2;
+  }
+  guard[0] = 0;
 
   int64_t out_src[NMOVE], out_dst[NMOVE], in_dst[NMOVE], first[NMOVE], valid[NMOVE];
   int32_t grp[NMOVE];
@@ -104,7 +117,7 @@ int main(int argc, char** argv) {
   /* 1. swap-out, and the same bytes moved by host loops */
   rc = aegkv_swap_blocks(NSEG, seg_bases, page_bytes, host_off, owners, NBLK, 1, kpp, host,
                          NHOST, composite, 0, NMOVE, out_src, out_dst, grp, first, valid, 0,
-                         AEGKV_MODE_AUTO, stream);
+                         AEGKV_MODE_AUTO, NULL, stream);
   if (rc) {
     fprintf(stderr, "swap-out: %d %s\n", rc, aegkv_last_error());
     return 1;
@@ -121,7 +134,7 @@ int main(int argc, char** argv) {
   /* 2. swap-in of those pages to other device blocks */
   rc = aegkv_swap_blocks(NSEG, seg_bases, page_bytes, host_off, owners, NBLK, 1, kpp, host,
                          NHOST, composite, 0, NMOVE, out_dst, in_dst, grp, first, valid, 1,
-                         AEGKV_MODE_AUTO, stream);
+                         AEGKV_MODE_AUTO, guard, stream);
   if (rc) {
     fprintf(stderr, "swap-in: %d %s\n", rc, aegkv_last_error());
     return 1;
@@ -164,9 +177,31 @@ int main(int argc, char** argv) {
   rc = compare_cache(seg_bases, "after the rejected call");
   if (rc) return rc;
 
+  /* 5. the guard set (as a failed fence wait would): the swap-in of the same
+   * pages to blocks 0..9 moves nothing */
+  __atomic_store_n(guard, 1, __ATOMIC_RELEASE);
+  int64_t low[NMOVE];
+  for (int i = 0; i < NMOVE; ++i) low[i] = i;
+  rc = aegkv_swap_blocks(NSEG, seg_bases, page_bytes, host_off, owners, NBLK, 1, kpp, host,
+                         NHOST, composite, 0, NMOVE, out_dst, low, grp, first, valid, 1,
+                         AEGKV_MODE_AUTO, guard, stream);
+  if (rc) {
+    fprintf(stderr, "guarded swap-in: %d %s\n", rc, aegkv_last_error());
+    return 1;
+  }
+  HIPCHK(hipStreamSynchronize(stream));
+  rc = compare_cache(seg_bases, "after the guarded swap-in");
+  if (rc) return rc;
+  printf("guarded swap-in moved nothing\n");
+
   free(want_host);
+  aegkv_host_free(guard);
   aegkv_host_free(host);
   for (int s = 0; s < NSEG; ++s) HIPCHK(hipFree(seg_bases[s]));
+  if (aegkv_stream_release(stream) != 0) {
+    fprintf(stderr, "aegkv_stream_release: %s\n", aegkv_last_error());
+    return 1;
+  }
   HIPCHK(hipStreamDestroy(stream));
   printf("c-abi ok\n");
   return 0;

@@ -1,0 +1,131 @@
+"""Config c4 at its full device size, run first of the GPU tests.
+
+The Qwen1.5-MoE shape needs 84 GiB of pinned host pages for its swaps, and
+these hosts cap the pinned memory of a process (a 63 GiB pool fits a fresh
+process, 73.5 GiB does not). Tests collect in file order, so this file runs
+before any other GPU test has pinned memory, and the swaps get the largest
+scale the host allows (3/4 on these hosts, as in bench.py --config overlap).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from aegaeon_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _kv_segments(n_layers, n_blocks, heads, dim, dtype, dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    segs = []
+    for _ in range(2 * n_layers):
+        t = torch.empty(n_blocks, 16, heads, dim, dtype=dtype, device=dev)
+        t.normal_(generator=g)
+        segs.append(t)
+    return segs
+
+
+def _pinned_pool_scaled(page, n_out, n_in, scales=(1.0, 0.875, 0.75, 0.625, 0.5)):
+    """The largest of `scales` whose swap blocks fit in one pinned pool on
+    this host. These hosts cap a process's pinned memory in total (a 63 GiB
+    pool fits a fresh process, 73.5 GiB does not), so pinned memory earlier
+    tests left in torch's host cache is released first."""
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
+    empty_host_cache = getattr(torch._C, "_host_emptyCache", None)   # torch's pinned cache
+    if empty_host_cache is not None:
+        empty_host_cache()
+    _say("torch host cache after release:",
+         {k: v for k, v in torch.cuda.host_memory_stats().items() if "current" in k})
+    for scale in scales:
+        o, i = int(n_out * scale), int(n_in * scale)
+        try:
+            return scale, o, i, ops.PinnedHostPool((o + i) * page)
+        except _lib.AegkvError as exc:
+            _say(f"pinned pool of {(o + i) * page} bytes refused ({exc}); scaling down")
+    pytest.fail(f"no pinned pool for the scales {scales}")
+
+
+def test_qwen15_moe_three_streams_at_config_size(gpu):
+    """Config c4 at its full device size: the Qwen1.5-MoE cache (48 x
+    [32768,16,16,128] bf16, 96 GiB) with swap-out, swap-in and copy_blocks of
+    2048 pairs on three streams at once. The swaps are 16384 out + 12288 in
+    (84 GiB of pinned pages) where the host pins that much, else the largest
+    of 7/8 ... 1/2 of them that fits beside what the process already pins
+    (these hosts pin 63 GiB but not 73.5 in a fresh process). Checked by
+    property: sampled host pages equal their source tiles, swap-in targets
+    equal the pages they came from, copy targets equal their sources, every
+    other block keeps its checksum."""
+    import time
+
+    t0 = time.perf_counter()
+    L, NB, H, D, NP = 24, 32768, 16, 128, 2048
+    segs = _kv_segments(L, NB, H, D, torch.bfloat16, gpu, 44)
+    S, tile = len(segs), 16 * H * D * 2
+    page = S * tile
+    scale, NOUT, NIN, pool = _pinned_pool_scaled(page, 16384, 12288)
+    _say(f"c4 at scale {scale}: swap-out {NOUT}, swap-in {NIN}, copy {NP} pairs; "
+         f"setup {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(44)
+    perm = rng.permutation(NB)
+    out_ids, in_ids = perm[:NOUT], perm[NOUT:NOUT + NIN]
+    csrc, cdst = perm[NOUT + NIN:NOUT + NIN + NP], perm[NOUT + NIN + NP:NOUT + NIN + 2 * NP]
+    hp = rng.permutation(NOUT + NIN)
+    hx, hy = hp[:NOUT], hp[NOUT:]
+    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
+    lay = ops.SegmentLayout(segs, *common)
+    zo, oo = np.zeros(NOUT, np.int32), np.ones(NOUT, np.int64)
+    zi, oi = np.zeros(NIN, np.int32), np.ones(NIN, np.int64)
+    # the incoming blocks: out to their host pages first, then cleared here
+    lay.swap(in_ids, hy, zi, zi, oi, False)
+    w = torch.arange(1, tile // 8 + 1, dtype=torch.int64, device=gpu)
+
+    def sums(t):   # per block: plain and position-weighted sums of its int64 words
+        x = t.view(NB, -1).view(torch.int64)
+        return torch.stack([x.sum(dim=1), (x * w).sum(dim=1)])
+
+    before = [sums(t) for t in segs]
+    di = torch.from_numpy(in_ids).to(gpu)
+    for t in segs:
+        t.index_fill_(0, di, 0)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(gpu) for _ in range(3)]
+    begin = torch.cuda.Event()
+    begin.record()
+    for st in streams:
+        st.wait_event(begin)
+    t1 = time.perf_counter()
+    with torch.cuda.stream(streams[0]):
+        lay.swap(out_ids, hx, zo, zo, oo, False)
+    with torch.cuda.stream(streams[1]):
+        lay.swap(hy, in_ids, zi, zi, oi, True)
+    with torch.cuda.stream(streams[2]):
+        ops.copy_blocks(segs, csrc, cdst)
+    torch.cuda.synchronize()
+    _say(f"three streams took {time.perf_counter() - t1:.2f} s")
+    moved = np.zeros(NB, bool)
+    moved[cdst] = True
+    keep = torch.from_numpy(~moved).to(gpu)
+    dcs, dcd = torch.from_numpy(csrc).to(gpu), torch.from_numpy(cdst).to(gpu)
+    for s_, t in enumerate(segs):
+        now = sums(t)
+        assert torch.equal(now[:, keep], before[s_][:, keep]), s_   # swap-in targets included
+        assert torch.equal(t[dcd], t[dcs]), s_
+    pages = pool.tensor.view(NOUT + NIN, S, tile)
+    for k in rng.choice(NOUT, 48, replace=False):
+        got = pages[int(hx[k])].to(gpu)
+        want = torch.stack([t[int(out_ids[k])].reshape(-1).view(torch.uint8) for t in segs])
+        assert torch.equal(got, want), int(k)
+    del lay, pages
+    pool.free()
+    del segs, before, w
+    torch.cuda.empty_cache()      # the 96 GiB cache goes before the other GPU tests
+    _say(f"c4 test done in {time.perf_counter() - t0:.1f} s at swap scale {scale} "
+         f"({NOUT} out, {NIN} in)")

@@ -1242,104 +1242,6 @@ def test_three_stream_overlap_correctness(gpu):
     pool.free()
 
 
-def _pinned_pool_scaled(page, n_out, n_in, scales=(1.0, 0.875, 0.75, 0.625, 0.5)):
-    """The largest of `scales` whose swap blocks fit in one pinned pool on
-    this host. These hosts cap a process's pinned memory in total (a 63 GiB
-    pool fits a fresh process, 73.5 GiB does not), so pinned memory earlier
-    tests left in torch's host cache is released first."""
-    import gc
-
-    gc.collect()
-    torch.cuda.synchronize()
-    empty_host_cache = getattr(torch._C, "_host_emptyCache", None)   # torch's pinned cache
-    if empty_host_cache is not None:
-        empty_host_cache()
-    _say("torch host cache after release:",
-         {k: v for k, v in torch.cuda.host_memory_stats().items() if "current" in k})
-    for scale in scales:
-        o, i = int(n_out * scale), int(n_in * scale)
-        try:
-            return scale, o, i, ops.PinnedHostPool((o + i) * page)
-        except _lib.AegkvError as exc:
-            _say(f"pinned pool of {(o + i) * page} bytes refused ({exc}); scaling down")
-    pytest.fail(f"no pinned pool for the scales {scales}")
-
-
-def test_qwen15_moe_three_streams_at_config_size(gpu):
-    """Config c4 at its full device size: the Qwen1.5-MoE cache (48 x
-    [32768,16,16,128] bf16, 96 GiB) with swap-out, swap-in and copy_blocks of
-    2048 pairs on three streams at once. The swaps are 16384 out + 12288 in
-    (84 GiB of pinned pages) where the host pins that much, else the largest
-    of 7/8 ... 1/2 of them that fits beside what the process already pins
-    (these hosts pin 63 GiB but not 73.5 in a fresh process). Checked by
-    property: sampled host pages equal their source tiles, swap-in targets
-    equal the pages they came from, copy targets equal their sources, every
-    other block keeps its checksum."""
-    import time
-
-    t0 = time.perf_counter()
-    L, NB, H, D, NP = 24, 32768, 16, 128, 2048
-    segs = _kv_segments(L, NB, H, D, torch.bfloat16, gpu, 44)
-    S, tile = len(segs), 16 * H * D * 2
-    page = S * tile
-    scale, NOUT, NIN, pool = _pinned_pool_scaled(page, 16384, 12288)
-    _say(f"c4 at scale {scale}: swap-out {NOUT}, swap-in {NIN}, copy {NP} pairs; "
-         f"setup {time.perf_counter() - t0:.1f} s")
-    rng = np.random.default_rng(44)
-    perm = rng.permutation(NB)
-    out_ids, in_ids = perm[:NOUT], perm[NOUT:NOUT + NIN]
-    csrc, cdst = perm[NOUT + NIN:NOUT + NIN + NP], perm[NOUT + NIN + NP:NOUT + NIN + 2 * NP]
-    hp = rng.permutation(NOUT + NIN)
-    hx, hy = hp[:NOUT], hp[NOUT:]
-    common = ([tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1], pool.tensor, page, 0)
-    lay = ops.SegmentLayout(segs, *common)
-    zo, oo = np.zeros(NOUT, np.int32), np.ones(NOUT, np.int64)
-    zi, oi = np.zeros(NIN, np.int32), np.ones(NIN, np.int64)
-    # the incoming blocks: out to their host pages first, then cleared here
-    lay.swap(in_ids, hy, zi, zi, oi, False)
-    w = torch.arange(1, tile // 8 + 1, dtype=torch.int64, device=gpu)
-
-    def sums(t):   # per block: plain and position-weighted sums of its int64 words
-        x = t.view(NB, -1).view(torch.int64)
-        return torch.stack([x.sum(dim=1), (x * w).sum(dim=1)])
-
-    before = [sums(t) for t in segs]
-    di = torch.from_numpy(in_ids).to(gpu)
-    for t in segs:
-        t.index_fill_(0, di, 0)
-    torch.cuda.synchronize()
-    streams = [torch.cuda.Stream(gpu) for _ in range(3)]
-    begin = torch.cuda.Event()
-    begin.record()
-    for st in streams:
-        st.wait_event(begin)
-    t1 = time.perf_counter()
-    with torch.cuda.stream(streams[0]):
-        lay.swap(out_ids, hx, zo, zo, oo, False)
-    with torch.cuda.stream(streams[1]):
-        lay.swap(hy, in_ids, zi, zi, oi, True)
-    with torch.cuda.stream(streams[2]):
-        ops.copy_blocks(segs, csrc, cdst)
-    torch.cuda.synchronize()
-    _say(f"three streams took {time.perf_counter() - t1:.2f} s")
-    moved = np.zeros(NB, bool)
-    moved[cdst] = True
-    keep = torch.from_numpy(~moved).to(gpu)
-    dcs, dcd = torch.from_numpy(csrc).to(gpu), torch.from_numpy(cdst).to(gpu)
-    for s_, t in enumerate(segs):
-        now = sums(t)
-        assert torch.equal(now[:, keep], before[s_][:, keep]), s_   # swap-in targets included
-        assert torch.equal(t[dcd], t[dcs]), s_
-    pages = pool.tensor.view(NOUT + NIN, S, tile)
-    for k in rng.choice(NOUT, 48, replace=False):
-        got = pages[int(hx[k])].to(gpu)
-        want = torch.stack([t[int(out_ids[k])].reshape(-1).view(torch.uint8) for t in segs])
-        assert torch.equal(got, want), int(k)
-    del lay, pages
-    pool.free()
-    _say(f"c4 test done in {time.perf_counter() - t0:.1f} s")
-
-
 def _ipc_producer(q_in, q_out):
     """Child process: write a pattern into a block of the parent's cache
     after a long kernel, record an interprocess event behind it and hand out
@@ -1657,35 +1559,25 @@ def test_fence_orders_a_swap_after_another_streams_write(gpu):
 
 
 def test_fence_wait_gives_up_after_its_budget(gpu):
-    """An unsignalled fence ends the wait after the timeout, sets the flag,
-    and the swapper reports it once and clears it."""
-    from aegaeon_amd.cache_groups import CacheGroupRuntimeConfig
-    from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
-    from aegaeon_amd.swapper import FenceToken, KVSwapper
-
+    """An unsignalled fence ends the wait after its budget and sets the move
+    guard to 1, in device memory or in pinned host memory (GuardWords); the
+    guard is never cleared. What the swaps behind such a wait do is in
+    test_gpu_guards.py."""
     words = torch.zeros(4, dtype=torch.int64, device=gpu)
     flags = torch.zeros(2, dtype=torch.int64, device=gpu)
-    st = torch.cuda.Stream()
-    ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0.002, stream=st)
-    st.synchronize()
+    host_guard = ops.GuardWords(2)
+    st = ops.DedicatedStream(gpu)
+    ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0.002, stream=st.stream)
+    ops.fence_wait(words, 0, 5, host_guard.tensor, 0, timeout_s=0.002, stream=st.stream)
+    ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0.002, stream=st.stream)
+    st.stream.synchronize()
     assert flags.tolist() == [0, 1]
+    assert host_guard.value(0) == 1 and host_guard.value(1) == 0
     with pytest.raises(ValueError, match="timeout"):
-        ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0, stream=st)
+        ops.fence_wait(words, 0, 5, flags, 1, timeout_s=0, stream=st.stream)
     with pytest.raises(ValueError, match="index"):
         ops.fence_signal(words, 4, 1)
-
-    n_blocks, page = 8, 4096
-    cache = allocate_composite_cache([KVCacheTensorSpec(n_blocks * page, ("l0",))], n_blocks, gpu)
-    pool = ops.PinnedHostPool(4 * page)
-    sw = KVSwapper(cache, [{"l0"}], [CacheGroupRuntimeConfig("attention", 16, 16)], pool.tensor,
-                   fence_words=words, fence_slots=(0, 1), fence_timeout_s=0.002)
-    sw.swap_blocks([1], [2], [0], [0], [0], [1], [FenceToken(3, 9)], False)
-    assert sw.last_fence == FenceToken(0, 1)
-    with pytest.raises(RuntimeError, match="never signalled"):
-        sw.wait_for_all_move_out()
-    sw.wait_for_all_move_out()             # reported once, then cleared
-    assert int(words[0]) == 1              # the swap still signalled its own word
-    pool.free()
+    st.close()
 
 
 def test_same_process_fence_token_waits_on_the_producers_event(gpu):
@@ -1718,7 +1610,7 @@ def test_same_process_fence_token_waits_on_the_producers_event(gpu):
     a.swap_blocks([1], src, host, [0] * 30, [0] * 30, [1] * 30, [None], False)
     token = a.last_fence
     assert token == FenceToken(0, 1)
-    assert _local_fences[(words.data_ptr(), 0)][0] == 1
+    assert _local_fences[(words.data_ptr(), 0)][1][-1][0] == 1     # (count, event) history
     b.swap_blocks([1], host, dst, [0] * 30, [0] * 30, [1] * 30, [token], True)
     b.wait_for_all_move_in()               # raises if a fence wait had timed out
     assert time.perf_counter() - t0 < 10
@@ -1797,8 +1689,11 @@ def test_fence_publish_follows_stream_work(gpu):
     words = torch.zeros(2, dtype=torch.int64, device=gpu)
     flags = torch.zeros(1, dtype=torch.int64, device=gpu)
     hw = ops.HostFenceWords(2)
+    # hardware queues of their own: a waiting fence holds its queue, so a
+    # signal on a stream that shares it would run only after the time-out
+    owners = [ops.DedicatedStream(gpu), ops.DedicatedStream(gpu)]
     try:
-        a, b = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+        a, b = (o.stream for o in owners)
         torch.cuda.synchronize()
         ops.fence_wait(words, 0, 1, flags, timeout_s=60, stream=a)
         ops.fence_publish(hw, 1, 9, device=gpu, stream=a)
@@ -1813,6 +1708,8 @@ def test_fence_publish_follows_stream_work(gpu):
     finally:
         torch.cuda.synchronize()
         hw.close()
+        for o in owners:
+            o.close()
 
 
 def _reclaim_worker(q_in, q_out):

@@ -289,7 +289,7 @@ def test_early_validation_without_gpu(aegkv_lib):
     rc = lib.aegkv_copy_blocks(0, None, None, 1, 0, None, None, None)
     assert rc == _lib.EINVAL
     rc = lib.aegkv_swap_blocks(1, None, None, None, None, 1, 1, None, None, 1, 1, 0, 1, None,
-                               None, None, None, None, 0, 0, None)
+                               None, None, None, None, 0, 0, None, None)
     assert rc == _lib.EINVAL
     assert b"metadata" in lib.aegkv_last_error()
     with pytest.raises(ValueError):
@@ -348,12 +348,19 @@ def test_fence_rejections_before_any_hip_call(aegkv_lib):
     from aegaeon_amd import _lib
 
     lib = aegkv_lib
-    assert lib.aegkv_fence_signal(None, 1, None) == _lib.EINVAL
-    assert lib.aegkv_fence_signal(0x1004, 1, None) == _lib.EINVAL       # not 8-byte aligned
+    assert lib.aegkv_fence_signal(None, 1, None, None) == _lib.EINVAL
+    assert lib.aegkv_fence_signal(0x1004, 1, None, None) == _lib.EINVAL   # not 8-byte aligned
     assert b"aligned" in lib.aegkv_last_error()
+    # bit 62 is the failure mark: values stay below it
+    assert lib.aegkv_fence_signal(0x1000, 1 << 62, None, None) == _lib.EINVAL
+    assert b"2^62" in lib.aegkv_last_error()
+    assert lib.aegkv_fence_signal(0x1000, 0, None, None) == _lib.EINVAL
     assert lib.aegkv_fence_wait(0x1000, 1, 0, 0x2000, None) == _lib.ERANGE
     assert lib.aegkv_fence_wait(0x1000, 1, 601 * 10**6, 0x2000, None) == _lib.ERANGE
     assert lib.aegkv_fence_wait(None, 1, 1000, 0x2000, None) == _lib.EINVAL
+    assert lib.aegkv_fence_wait(0x1000, 1 << 62, 1000, 0x2000, None) == _lib.EINVAL
+    assert lib.aegkv_guard_merge(None, 0x2000, None) == _lib.EINVAL
+    assert lib.aegkv_guard_merge(0x1000, 0x2004, None) == _lib.EINVAL    # not 8-byte aligned
     from aegaeon_amd import ops
 
     with pytest.raises(ValueError, match="int64"):
@@ -362,6 +369,11 @@ def test_fence_rejections_before_any_hip_call(aegkv_lib):
         ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 1)
     with pytest.raises(ValueError, match="positive"):
         ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 0)
+    with pytest.raises(ValueError, match="2\\*\\*62"):
+        ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, ops.FENCE_FAILED)
+    with pytest.raises(ValueError, match="guard index"):
+        ops.fence_signal(torch.zeros(4, dtype=torch.int64), 0, 1,
+                         guard=torch.zeros(2, dtype=torch.int64), guard_index=2)
 
 
 def test_host_fence_words_across_processes(aegkv_lib):
@@ -401,10 +413,11 @@ def test_host_fence_rejections_before_any_hip_call(aegkv_lib):
     lib = aegkv_lib
     word = (ctypes.c_uint64 * 2)()
     base = ctypes.addressof(word)
-    assert lib.aegkv_fence_publish(None, 1, None) == _lib.EINVAL
-    assert lib.aegkv_fence_publish(base + 4, 1, None) == _lib.EINVAL
-    assert lib.aegkv_fence_publish(base, 0, None) == _lib.EINVAL
-    assert lib.aegkv_fence_publish(base, 1 << 63, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(None, 1, None, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base + 4, 1, None, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base, 0, None, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base, 1 << 62, None, None) == _lib.EINVAL
+    assert lib.aegkv_fence_publish(base, 1, base + 12, None) == _lib.EINVAL   # guard unaligned
     assert lib.aegkv_fence_host_wait(None, 1, 0) == _lib.EINVAL
     assert lib.aegkv_fence_host_wait(base + 1, 1, 0) == _lib.EINVAL
     assert lib.aegkv_fence_host_wait(base, 1, -1) == _lib.ERANGE
@@ -412,6 +425,10 @@ def test_host_fence_rejections_before_any_hip_call(aegkv_lib):
     word[0] = 5
     assert lib.aegkv_fence_host_wait(base, 5, 0) == 1
     assert lib.aegkv_fence_host_wait(base, 6, 1000) == 0
+    # a word with the failure mark answers "failed" (2) whatever the count
+    word[0] = 3 | (1 << 62)
+    assert lib.aegkv_fence_host_wait(base, 2, 0) == 2
+    assert lib.aegkv_fence_host_wait(base, 9, 1000) == 2
 
 
 def test_local_fence_entries_end_with_their_swapper():
@@ -438,6 +455,38 @@ def test_local_fence_entries_end_with_their_swapper():
     gc.collect()
     assert swm._local_fence_event(addr, 3, 1) is None
     assert (addr, 3) not in swm._local_fences
+
+
+def test_local_fence_waits_on_the_move_the_token_names():
+    """A token for count k is waited on through the event of count k (the
+    first recorded count >= k), not through the latest swap's, so a consumer
+    does not wait for later swaps queued on the producer's stream; once the
+    history has dropped count k, the oldest kept event (later than k) stands
+    in, which still orders the consumer after move k."""
+    from aegaeon_amd import swapper as swm
+
+    class Raiser:
+        pass
+
+    raiser = Raiser()
+    addr = 0x7F00_0000_2000
+    events = {c: object() for c in range(1, 200)}
+    for c in (1, 2, 3):
+        swm._note_local_fence(addr, 0, c, events[c], raiser)
+    assert swm._local_fence_event(addr, 0, 1) is events[1]
+    assert swm._local_fence_event(addr, 0, 2) is events[2]
+    assert swm._local_fence_event(addr, 0, 3) is events[3]
+    for c in range(4, 200):
+        swm._note_local_fence(addr, 0, c, events[c], raiser)
+    oldest = 200 - swm._LOCAL_FENCE_HISTORY
+    assert swm._local_fence_event(addr, 0, 1) is events[oldest]      # trimmed: a later one
+    assert swm._local_fence_event(addr, 0, 150) is events[150]
+    assert swm._local_fence_event(addr, 0, 200) is None
+    # another swapper raising the same words (the old one gone) starts afresh
+    other = Raiser()
+    swm._note_local_fence(addr, 0, 1, events[1], other)
+    assert swm._local_fence_event(addr, 0, 150) is None
+    del swm._local_fences[(addr, 0)]
 
 
 def test_tuning_knobs(aegkv_lib):
@@ -512,7 +561,7 @@ def _swap_blocks_call(lib, *, n_seg=2, page=(4096, 4096), hoff=(0, 4096), owners
         n_seg, bases, p(keep[0]), p(keep[1]), p(keep[2], ctypes.POINTER(ctypes.c_uint64)),
         dev_blocks, len(kpp), p(keep[3]), ctypes.c_void_p(0x7000000), host_blocks, host_page,
         rank_off, len(src), p(keep[4]), p(keep[5]), p(keep[6], ctypes.POINTER(ctypes.c_int32)),
-        p(keep[7]), p(keep[8]), is_in, mode, None)
+        p(keep[7]), p(keep[8]), is_in, mode, None, None)
 
 
 @pytest.mark.parametrize("kwargs,code,word", [
@@ -724,7 +773,7 @@ def test_host_alloc_flags_rejections(aegkv_lib):
     from aegaeon_amd import _lib
 
     p = ctypes.c_void_p()
-    assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 4096, 2) == _lib.EINVAL
+    assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 4096, 4) == _lib.EINVAL
     assert b"flags" in aegkv_lib.aegkv_last_error()
     assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 0, 1) == _lib.EINVAL
     assert aegkv_lib.aegkv_host_alloc_flags(None, 16, 1) == _lib.EINVAL
@@ -746,7 +795,7 @@ def test_migrate_blocks_rejections_before_any_hip_call(aegkv_lib):
     def call(src_b, dst_b, src, dst, n_src=8, n_dst=8, n_seg=2):
         s, d = np.array(src, np.int64), np.array(dst, np.int64)
         return lib.aegkv_migrate_blocks(n_seg, src_b, dst_b, p64(page), n_src, n_dst, s.size,
-                                        p64(s), p64(d), None)
+                                        p64(s), p64(d), None, None)
 
     assert call(A, B, [1], [2], n_seg=0) == _lib.EINVAL
     assert call(None, B, [1], [2]) == _lib.EINVAL
@@ -756,3 +805,64 @@ def test_migrate_blocks_rejections_before_any_hip_call(aegkv_lib):
     assert call(A, B, [1], [3], n_dst=3) == _lib.ERANGE   # target id past the target cache
     assert call(A, B, [1, 2], [5, 5]) == _lib.EDUP
     assert call(A, B, [], []) == _lib.OK                   # nothing to move, no GPU needed
+
+
+def test_launch_item_bound_before_any_hip_call(aegkv_lib):
+    """The kernels walk their work items with a 32-bit grid-stride loop, so a
+    launch may hold at most 2^32 - 1 - (2^32 - 1) // 256 items (the item
+    index plus the largest grid then stays below 2^32 and the loop cannot
+    wrap). Calls over that bound are refused before any HIP call; a call at
+    exactly the bound passes it and only then meets the device checks (which
+    fail here, with no GPU: the fake bases are not device memory). The sizes
+    come from huge page sizes over placeholder pointers that nothing
+    dereferences."""
+    from aegaeon_amd import _lib
+
+    lib = aegkv_lib
+    limit = (2**32 - 1) - (2**32 - 1) // 256
+    assert limit == 4_278_190_080 == 255 << 24
+    p64 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))  # noqa: E731
+    src, dst = np.array([0], np.int64), np.array([1], np.int64)
+
+    def copy(entry, n_seg, page):
+        bases = (ctypes.c_void_p * n_seg)(*[0x10000 * (i + 1) for i in range(n_seg)])
+        pages = np.full(n_seg, page, np.int64)
+        if entry == "migrate":
+            other = (ctypes.c_void_p * n_seg)(*[(1 << 60) + 0x10000 * i
+                                                for i in range(n_seg)])
+            return lib.aegkv_migrate_blocks(n_seg, bases, other, p64(pages), 2, 2, 1, p64(src),
+                                            p64(dst), None, None)
+        return getattr(lib, entry)(n_seg, bases, p64(pages), 2, 1, p64(src), p64(dst), None)
+
+    # copy shapes: a page of 2^24 x 10 rows of 16 KiB moves 10 rows per item
+    # (2^24 items per tile); a page of (limit + 1) rows of 16 KiB (not a
+    # multiple of 2, 3 or 5) moves one row per item
+    at_limit = ((limit // 10) * 10 * 16384, 10)      # 10 segments x limit/10 items
+    over = ((limit + 1) * 16384, 1)                  # 1 segment x (limit + 1) items
+    for entry in ("aegkv_copy_blocks", "aegkv_copy_blocks_noalloc", "migrate"):
+        page, n_seg = over
+        assert copy(entry, n_seg, page) == _lib.EINVAL, entry
+        assert b"work items of one launch" in lib.aegkv_last_error(), entry
+        page, n_seg = at_limit
+        rc = copy(entry, n_seg, page)
+        assert rc == _lib.EINVAL and b"device memory" in lib.aegkv_last_error(), (entry, rc)
+
+    # swap kernels move 8 KiB per item (256 lanes x 2 loads of 16 B)
+    for items, refused in ((limit + 1, True), (limit, False)):
+        page = items * 8192
+        rc = _swap_blocks_call(lib, n_seg=1, page=(page,), hoff=(0,), owners=(1,), kpp=(1,),
+                               host_page=page, dev_blocks=2, host_blocks=1, src=(0,), dst=(0,),
+                               valid=(1,))
+        assert rc == _lib.EINVAL
+        msg = lib.aegkv_last_error()
+        assert (b"work items of one launch" in msg) == refused, msg
+
+    # weight slices: 8 KiB per item as well
+    for items, refused in ((limit + 1, True), (limit, False)):
+        d = (ctypes.c_void_p * 1)(0x10000)
+        h = (ctypes.c_void_p * 1)(0x20000)
+        b = np.array([items * 8192], np.int64)
+        rc = lib.aegkv_load_slices(1, d, h, p64(b), 1, None)
+        assert rc == _lib.EINVAL
+        msg = lib.aegkv_last_error()
+        assert (b"work items of one launch" in msg) == refused, msg
