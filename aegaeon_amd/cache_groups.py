@@ -43,23 +43,24 @@ def _check_group(kind: str, block: int, kernel: int, window: Optional[int],
                  block_name: str) -> None:
     if block <= 0 or kernel <= 0:
         raise ValueError(
-            f"Cache block sizes must both be positive: {block_name}={block}, kernel={kernel}"
+            f"{block_name} block of {block} tokens and kernel block of {kernel}: both "
+            "need to be above zero"
         )
     if kind == "attention":
         if block % kernel:
             raise ValueError(
-                f"Attention kernel block size {kernel} must divide {block_name} "
-                f"block size {block}"
+                f"an attention {block_name} block of {block} tokens does not hold whole "
+                f"{kernel}-token kernel blocks"
             )
     elif kind == "mamba_none":
         if block != kernel:
-            raise ValueError("Mamba/GDN state pages cannot be split into kernel blocks")
+            raise ValueError("a state-page (mamba_none) group keeps one kernel block per page")
         if window is not None:
-            raise ValueError("Mamba/GDN cache groups cannot have a sliding window")
+            raise ValueError("a state-page (mamba_none) group takes no sliding window")
     else:
-        raise NotImplementedError(f"Unsupported cache group kind: {kind}")
+        raise NotImplementedError(f"cache group kind {kind!r} is not one this planner knows")
     if window is not None and window <= 0:
-        raise ValueError(f"sliding_window must be positive, got {window}")
+        raise ValueError(f"a sliding window of {window} tokens is not above zero")
 
 
 @dataclass
@@ -81,7 +82,7 @@ class CacheGroupConfig:
 
     def table_blocks_for_tokens(self, num_tokens: int) -> int:
         if num_tokens < 0:
-            raise ValueError(f"num_tokens must be non-negative, got {num_tokens}")
+            raise ValueError(f"{num_tokens} tokens is negative")
         if self.kind == "attention":
             return logical_blocks_for_tokens(num_tokens, self.block_size)
         return 1
@@ -89,7 +90,7 @@ class CacheGroupConfig:
     def blocks_for_tokens(self, num_tokens: int) -> int:
         """Resident-page bound used for admission (block_manager.py:173-194)."""
         if num_tokens < 0:
-            raise ValueError(f"num_tokens must be non-negative, got {num_tokens}")
+            raise ValueError(f"{num_tokens} tokens is negative")
         if self.kind == "mamba_none":
             return 1
         if self.sliding_window is None:
@@ -99,10 +100,7 @@ class CacheGroupConfig:
 
     def num_skipped_blocks(self, processed_computed_tokens: int) -> int:
         if processed_computed_tokens < 0:
-            raise ValueError(
-                "processed_computed_tokens must be non-negative, got "
-                f"{processed_computed_tokens}"
-            )
+            raise ValueError(f"{processed_computed_tokens} processed tokens is negative")
         if self.kind != "attention" or self.sliding_window is None:
             return 0
         return num_skipped_sliding_window_blocks(processed_computed_tokens, self.block_size,
@@ -110,9 +108,7 @@ class CacheGroupConfig:
 
     def block_is_skipped(self, processed_computed_tokens: int, logical_block_index: int) -> bool:
         if logical_block_index < 0:
-            raise ValueError(
-                f"logical_block_index must be non-negative, got {logical_block_index}"
-            )
+            raise ValueError(f"logical block {logical_block_index} is negative")
         return logical_block_index < self.num_skipped_blocks(processed_computed_tokens)
 
     @property
@@ -130,9 +126,9 @@ class CacheGroupConfig:
 
     def valid_kernel_blocks(self, cached_tokens: int, block_index: int) -> int:
         if cached_tokens < 0:
-            raise ValueError(f"cached_tokens must be non-negative, got {cached_tokens}")
+            raise ValueError(f"{cached_tokens} cached tokens is negative")
         if block_index < 0:
-            raise ValueError(f"block_index must be non-negative, got {block_index}")
+            raise ValueError(f"block {block_index} is negative")
         if self.kind == "mamba_none":
             return 1
         return self.kernel_block_extent(cached_tokens, block_index)[1]
@@ -178,19 +174,19 @@ class CacheGroupRuntimeConfig:
     def slot_for_position(self, kv_block_ids: Sequence[int], position: int) -> int:
         """Token position -> slot in the kernel-shaped cache (block_manager.py:357-382)."""
         if self.kind != "attention":
-            raise ValueError(f"Cache group {self.kind} has no token slot mapping")
+            raise ValueError(f"a {self.kind} group maps no token positions to slots")
         if position < 0:
-            raise ValueError(f"Token position must be non-negative, got {position}")
+            raise ValueError(f"token position {position} is negative")
         column, inside = divmod(position, self.kv_block_size)
         if column >= len(kv_block_ids):
             raise IndexError(
-                f"Position {position} needs physical table column {column}, "
-                f"but the table has {len(kv_block_ids)} columns"
+                f"token {position} falls in column {column} of a "
+                f"{len(kv_block_ids)}-column table"
             )
         pid = kv_block_ids[column]
         if pid < 0:
             raise RuntimeError(
-                f"Position {position} maps to released logical table column {column}"
+                f"token {position} falls in column {column}, which was released"
             )
         kernel_id = pid * self.blocks_per_kv_block + inside // self.kernel_block_size
         return kernel_id * self.kernel_block_size + inside % self.kernel_block_size
@@ -213,7 +209,7 @@ class BlockTable:
     def replace_flat_blocks(self, blocks: List[int]) -> None:
         live = sum(b != LOGICAL_NULL_BLOCK_ID for col in self.group_blocks for b in col)
         if len(blocks) != live:
-            raise ValueError(f"Expected {live} blocks, got {len(blocks)}")
+            raise ValueError(f"{len(blocks)} ids for a table with {live} live columns")
         it = iter(blocks)
         self.group_blocks = [
             [b if b == LOGICAL_NULL_BLOCK_ID else next(it) for b in col]
@@ -252,7 +248,7 @@ class BlockTable:
         rows = self.transfer_entries(processed_computed_tokens)
         if len(rows) != len(target_block_ids):
             raise ValueError(
-                f"Expected {len(rows)} target blocks, got {len(target_block_ids)}"
+                f"{len(target_block_ids)} target ids for {len(rows)} retained pages"
             )
         moved = [[LOGICAL_NULL_BLOCK_ID] * len(col) for col in self.group_blocks]
         for (g, i, _, _, _), tid in zip(rows, target_block_ids):

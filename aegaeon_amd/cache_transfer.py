@@ -14,12 +14,12 @@ from __future__ import annotations
 
 def _need_nonneg(name: str, value: int) -> None:
     if value < 0:
-        raise ValueError(f"{name} must be non-negative, got {value}")
+        raise ValueError(f"{name} = {value} is negative")
 
 
 def _need_pos(name: str, value: int) -> None:
     if value <= 0:
-        raise ValueError(f"{name} must be positive, got {value}")
+        raise ValueError(f"{name} = {value} is not above zero")
 
 
 def _ceil_div(a: int, b: int) -> int:
@@ -75,11 +75,12 @@ def kernel_block_extent_for_attention_page(
     _need_nonneg("cached_tokens", cached_tokens)
     _need_nonneg("physical_block_index", physical_block_index)
     if physical_block_size <= 0 or kernel_block_size <= 0:
-        raise ValueError("physical and kernel block sizes must be positive")
+        raise ValueError(f"block sizes need to be > 0 (physical {physical_block_size}, "
+                         f"kernel {kernel_block_size})")
     if physical_block_size % kernel_block_size:
         raise ValueError(
-            f"Kernel block size {kernel_block_size} must divide physical "
-            f"block size {physical_block_size}"
+            f"a {physical_block_size}-token physical block does not hold a whole number of "
+            f"{kernel_block_size}-token kernel blocks"
         )
     if sliding_window is not None:
         _need_pos("sliding_window", sliding_window)
@@ -112,12 +113,12 @@ def prefix_bytes_for_kernel_blocks(page_size_bytes: int, kernel_blocks_per_page:
     _need_pos("kernel_blocks_per_page", kernel_blocks_per_page)
     if not 0 <= valid_kernel_blocks <= kernel_blocks_per_page:
         raise ValueError(
-            f"valid kernel blocks {valid_kernel_blocks} outside [0, {kernel_blocks_per_page}]"
+            f"{valid_kernel_blocks} live kernel blocks for a page of {kernel_blocks_per_page}"
         )
     if page_size_bytes % kernel_blocks_per_page:
         raise ValueError(
-            f"Backing page size {page_size_bytes} is not divisible by "
-            f"{kernel_blocks_per_page} kernel blocks"
+            f"a {page_size_bytes}-byte page does not split into {kernel_blocks_per_page} "
+            f"equal kernel blocks"
         )
     return (page_size_bytes // kernel_blocks_per_page) * valid_kernel_blocks
 
@@ -131,8 +132,8 @@ def byte_extent_for_kernel_blocks(page_size_bytes: int, kernel_blocks_per_page: 
     last = first_kernel_block + num_kernel_blocks
     if last > kernel_blocks_per_page:
         raise ValueError(
-            f"Kernel-block extent [{first_kernel_block}, {last}) "
-            f"exceeds page size {kernel_blocks_per_page}"
+            f"kernel blocks [{first_kernel_block}, {last}) run past a page of "
+            f"{kernel_blocks_per_page}"
         )
     return (
         prefix_bytes_for_kernel_blocks(page_size_bytes, kernel_blocks_per_page,

@@ -1019,7 +1019,7 @@ int validate_layout(const SwapLayout& L, int64_t* composite_bytes, bool* dev_vec
     for (int32_t g = 0; g < L.num_groups; ++g)
       if (((L.owner_masks[s] >> g) & 1ull) && pb % L.kpp[g] != 0)
         return fail(AEGKV_EEXTENT,
-                    "segment %d page of %lld bytes is not divisible by %lld kernel blocks", s,
+                    "segment %d page of %lld bytes does not split into %lld equal kernel blocks", s,
                     static_cast<long long>(pb), static_cast<long long>(L.kpp[g]));
     if (L.num_groups < 64 && (L.owner_masks[s] >> L.num_groups) != 0)
       return fail(AEGKV_ERANGE, "segment %d owner mask names a group >= %d", s, L.num_groups);
@@ -1076,7 +1076,7 @@ int validate_list(const SwapLayout& L, const SwapList& E, bool is_swap_in) {
     const int64_t first = E.first ? E.first[i] : 0;
     const int64_t valid = E.valid ? E.valid[i] : k;
     if (first < 0 || valid < 0 || first > k || valid > k - first)
-      return fail(AEGKV_EEXTENT, "kernel-block extent [%lld, %lld) at %lld exceeds page size %lld",
+      return fail(AEGKV_EEXTENT, "kernel blocks [%lld, %lld) of entry %lld run past a page of %lld",
                   static_cast<long long>(first), static_cast<long long>(first + valid),
                   static_cast<long long>(i), static_cast<long long>(k));
   }

@@ -43,21 +43,22 @@ def make_composite_layout(tensor_specs: Sequence[KVCacheTensorSpec], num_blocks:
     """Segments in tensor order and the composite page size
     (vllm_cache.py:75-101, including its three rejections)."""
     if num_blocks <= 0:
-        raise MemoryError(f"Not enough cache memory for one cache block: blocks={num_blocks}")
+        raise MemoryError(f"a cache of {num_blocks} blocks holds no block")
     segments: List[CacheSegment] = []
     offset = 0
     for spec in tensor_specs:
         if spec.block_stride > 0:
             raise NotImplementedError(
-                "swap does not support the packed KV-cache backing layout"
+                "a backing tensor with a block stride (packed K/V) has no per-block page "
+                "for the swaps"
             )
         if spec.size % num_blocks:
             raise ValueError(
-                "KV-cache tensor size must contain an integral page per block: "
-                f"size={spec.size}, blocks={num_blocks}"
+                f"a {spec.size}-byte backing tensor does not split into {num_blocks} "
+                "equal block pages"
             )
         if not spec.shared_by:
-            raise ValueError("KV-cache tensor is not bound to any layer")
+            raise ValueError("a backing tensor with no layer names")
         page = spec.size // num_blocks
         segments.append(CacheSegment(spec.shared_by[0], tuple(spec.shared_by), offset, page))
         offset += page
@@ -142,6 +143,7 @@ def host_page_geometry(composite_page_bytes: int, tp_size: int, element_size: in
     total = composite_page_bytes * tp_size
     if total % element_size:
         raise ValueError(
-            f"Composite cache page {total} is not aligned to CPU cache dtype size {element_size}"
+            f"a {total}-byte host page is not a whole number of {element_size}-byte "
+            "host elements"
         )
     return total

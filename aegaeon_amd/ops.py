@@ -230,9 +230,8 @@ class SegmentLayout:
         valid = _i64(valid_kernel_blocks)
         if not (src.size == dst.size == grp.size == first.size == valid.size):
             raise ValueError(
-                "Swap block ids and metadata must have equal lengths: "
-                f"source={src.size}, target={dst.size}, groups={grp.size}, "
-                f"first={first.size}, valid={valid.size}"
+                f"swap lists of unequal lengths: {src.size} sources, {dst.size} targets, "
+                f"{grp.size} groups, {first.size} first and {valid.size} valid kernel blocks"
             )
         gp = _guard_ptr(guard, guard_index, "guard")
         lib = _lib.load()

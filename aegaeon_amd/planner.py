@@ -86,17 +86,17 @@ class BlockPools:
         """
         if num_max_blocks <= 1:
             raise ValueError(
-                "GPU cache must contain at least one usable block in addition to the "
-                "reserved null block"
+                f"a GPU cache of {num_max_blocks} blocks has no block besides the null "
+                "block 0"
             )
         if not cache_groups:
-            raise ValueError("GPU cache must expose at least one cache group")
+            raise ValueError("a GPU cache space needs at least one cache group")
         if engine_id in self.gpu_free_blocks and block_tables is not None:
             for rid, table in block_tables.items():
                 if table.location == engine_id:
                     raise ValueError(
-                        f"Error registering new GPU cache space for engine_id {engine_id}; "
-                        f"Request #{rid} still resides in the cache."
+                        f"engine {engine_id}'s cache space cannot be replaced while "
+                        f"request {rid} has blocks in it"
                     )
         self.move_events_gpu.pop(engine_id, None)
         self.move_gpu_num_blocks[engine_id] = 0
@@ -139,15 +139,15 @@ class BlockPools:
         block_shape = tuple(block_shape)
         if is_gpu(location):
             if location not in self.gpu_free_blocks:
-                raise KeyError(f"unknown gpu location {location}")
+                raise KeyError(f"no GPU cache space registered for engine {location}")
             free = self.gpu_free_blocks[location]
             if len(free) < num_blocks:
                 # wait for this engine's swap-outs and take back their sources
                 self.reclaim_gpu_moves(location, wait=True)
             if len(free) < num_blocks:
                 raise ResourceWarning(
-                    f"not enough free blocks on GPU, requested {num_blocks}, "
-                    f"available {len(free)}"
+                    f"engine {location} has {len(free)} free blocks, {num_blocks} "
+                    "asked for"
                 )
             out = free[:num_blocks]
             del free[:num_blocks]
@@ -160,8 +160,8 @@ class BlockPools:
             self.reclaim_cpu_moves(block_shape, wait=True)
         if not self._cpu_blocks_available(block_bytes, num_blocks - len(free)):
             raise ResourceWarning(
-                f"not enough free blocks on CPU, requested {num_blocks}, available "
-                f"{len(free)} and {len(self.cpu_free_slabs)} slabs"
+                f"the host pool has {len(free)} free blocks and "
+                f"{len(self.cpu_free_slabs)} free slabs, {num_blocks} blocks asked for"
             )
         while len(free) < num_blocks:
             slab = self.cpu_free_slabs.pop()
@@ -433,7 +433,7 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
         if table.location == target_location:
             continue
         if is_gpu(table.location) and is_gpu(target_location):
-            raise NotImplementedError("Migration is not implemented")
+            raise NotImplementedError("GPU to GPU moves go through plan_migrate")
         if src_loc is not None and table.location != src_loc:
             raise ValueError(f"request {rid} is on {table.location}; expected {src_loc}")
         if shape is not None and tuple(table.block_shape) != shape:
@@ -444,7 +444,7 @@ def plan_move(requests: Sequence[Tuple[int, int]], block_tables: Dict[int, Block
             groups = pools.gpu_cache_groups.get(target_location)
             if tuple(table.cache_groups) != groups:
                 raise ValueError(
-                    f"request {rid} cache groups do not match target engine #{target_location}"
+                    f"request {rid}'s cache groups differ from engine {target_location}'s"
                 )
         plans.append((table, tokens, None))
         moved_ids.append(rid)
@@ -523,7 +523,7 @@ def plan_migrate(requests: Sequence[int], block_tables: Dict[int, BlockTable],
             raise ValueError(f"request {rid}'s shape is not {shape}")
         if tuple(table.cache_groups) != pools.gpu_cache_groups.get(target_location):
             raise ValueError(
-                f"request {rid} cache groups do not match target engine #{target_location}")
+                f"request {rid}'s cache groups differ from engine {target_location}'s")
         src_loc = table.location
         shape = tuple(table.block_shape)
         tables.append((rid, table))

@@ -231,8 +231,7 @@ class KVSwapper:
             owners = frozenset(g for g, names in enumerate(group_layer_names)
                                if set(seg.shared_by) & set(names))
             if not owners:
-                raise ValueError(f"Cache segment {seg.layer_name} is not owned by any "
-                                 "KV-cache group")
+                raise ValueError(f"no cache group names a layer of segment {seg.layer_name}")
             self.segment_group_ids.append(owners)
         # host view (worker.py:1419-1432)
         self.host_page_bytes = host_page_geometry(cache.page_size_bytes, tp_size,
@@ -254,8 +253,8 @@ class KVSwapper:
             for g in owners:
                 if self._page[s] % self._kpp[g]:
                     raise ValueError(
-                        f"Backing page size {int(self._page[s])} is not divisible by "
-                        f"{int(self._kpp[g])} kernel blocks"
+                        f"segment {s}'s {int(self._page[s])}-byte page does not split into "
+                        f"{int(self._kpp[g])} equal kernel blocks"
                     )
         # bytes and extents one entry of group g moves per kernel block
         n_groups = len(self.group_descriptors)
@@ -350,10 +349,10 @@ class KVSwapper:
                    len(first_kernel_blocks), len(valid_kernel_blocks)}
         if len(lengths) != 1:
             raise ValueError(
-                "Swap block ids and metadata must have equal lengths: "
-                f"source={len(source_block_ids)}, target={len(target_block_ids)}, "
-                f"groups={len(group_ids)}, first={len(first_kernel_blocks)}, "
-                f"valid={len(valid_kernel_blocks)}"
+                f"swap lists of unequal lengths: {len(source_block_ids)} sources, "
+                f"{len(target_block_ids)} targets, {len(group_ids)} groups, "
+                f"{len(first_kernel_blocks)} first and {len(valid_kernel_blocks)} valid "
+                "kernel blocks"
             )
         self._require_open()
         groups = np.asarray(group_ids, dtype=np.int64).reshape(-1)
@@ -379,9 +378,9 @@ class KVSwapper:
             extents = int(((valid > 0) * self._extents_per_entry[groups]).sum()) if groups.size else 0
             full = len(source_block_ids) * self.cache.page_size_bytes
             saved = 0.0 if full == 0 else 1.0 - copied / full
-            logger.info("swap requests %s (%s to %s): copied %d/%d bytes (saved %.2f%%), "
-                        "%d extents in one launch", list(request_ids),
-                        "CPU" if is_swap_in else "GPU", "GPU" if is_swap_in else "CPU",
+            logger.info("requests %s moved %s: %d of %d page bytes (%.2f%% skipped), "
+                        "%d extents, one launch", list(request_ids),
+                        "host->device" if is_swap_in else "device->host",
                         copied, full, saved * 100, extents)
         return new_event
 

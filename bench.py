@@ -84,7 +84,7 @@ def parse():
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
     p.add_argument("--config", default="headline",
                    choices=["headline", "varlen", "overlap", "refplan", "switch", "serving",
-                            "tiles"],
+                            "tiles", "copy-beside-swaps"],
                    help="headline: Qwen3-4B swaps + Llama-2-13B copy_blocks (the metric line); "
                         "varlen: Qwen2.5-7B variable-length batched swap; overlap: "
                         "Qwen1.5-MoE swap-out + swap-in + copy_blocks on three streams; "
@@ -93,8 +93,17 @@ def parse():
                         "two models' KV swapped out and in at once through the planner, "
                         "swapper and move ledger; serving: a bf16 GEMM loop beside both "
                         "swaps, for the default and a smaller swap grid; tiles: copy_blocks "
-                        "by tile size (16-160 KiB) beside its read-only and write-only probes")
+                        "by tile size (16-160 KiB) beside its read-only and write-only probes; "
+                        "copy-beside-swaps: an HBM copy beside the swap kernels by swap grid")
     return p.parse_args()
+
+
+def log_pinned(ops, where):
+    """Pinned host memory the library holds (what counts against the host's
+    per-process cap), on stderr."""
+    pinned, free = ops.host_pinned_usage()
+    log(f"pinned host memory {where}: {pinned / 2**30:.2f} GiB held, "
+        f"{free / 2**30:.2f} GiB of it free for uncached pools")
 
 
 def kv_segments(torch, n_layers, n_blocks, heads, dim, dtype, dev, seed):
@@ -514,34 +523,64 @@ def bench_overlap(args):
         t.index_fill_(0, di, 0)
     torch.cuda.synchronize()
     # Three streams with hardware queues of their own; three runs, the
-    # medians reported.
+    # medians reported, for two swap grids: the library's defaults (sized
+    # for the link alone) and 16 workgroups per swap kernel (128 KiB in
+    # flight per direction), which leaves the L2 channels' memory request
+    # queues to the copy: beyond about 16-24 workgroups the swap kernels'
+    # host-bound requests, which take microseconds to complete, fill those
+    # queues and the copy's HBM requests wait behind them.
     streams = [o.stream for o in owners]
-    runs = []
+    grid_keys = (_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_SWAP_IN_WORKGROUPS)
+    default_grid = tuple(_lib.tune(k) for k in grid_keys)
+    shared_grid = (16, 16)
+
+    def three_streams(grid):
+        for k, v in zip(grid_keys, grid):
+            _lib.tune(k, v)
+        runs = []
+        for _ in range(3):
+            evs = [ev_pair(torch) for _ in range(3)]
+            begin = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            begin.record()
+            for st in streams:
+                st.wait_event(begin)
+            with torch.cuda.stream(streams[0]):
+                evs[0][0].record()
+                lay.swap(out_ids, host_x, zo, zo, oo, False)
+                evs[0][1].record()
+            with torch.cuda.stream(streams[1]):
+                evs[1][0].record()
+                lay.swap(host_y, in_ids, zi, zi, oi, True)
+                evs[1][1].record()
+            with torch.cuda.stream(streams[2]):
+                evs[2][0].record()
+                ops.copy_blocks(segs, csrc, cdst)
+                evs[2][1].record()
+            torch.cuda.synchronize()
+            runs.append((evs[0][0].elapsed_time(evs[0][1]) / 1e3,
+                         evs[1][0].elapsed_time(evs[1][1]) / 1e3,
+                         evs[2][0].elapsed_time(evs[2][1]) / 1e3,
+                         max(begin.elapsed_time(e[1]) for e in evs) / 1e3))
+        return tuple(statistics.median(r[i] for r in runs) for i in range(4))
+
+    try:
+        t_out, t_in, t_cp, span = three_streams(shared_grid)
+        d_out, d_in, d_cp, d_span = three_streams(default_grid)
+    finally:
+        for k, v in zip(grid_keys, default_grid):
+            _lib.tune(k, v)
+    # the same copy alone on its stream (same CUs), for comparison
+    alone = []
     for _ in range(3):
-        evs = [ev_pair(torch) for _ in range(3)]
-        begin = torch.cuda.Event(enable_timing=True)
+        a, b = ev_pair(torch)
         torch.cuda.synchronize()
-        begin.record()
-        for st in streams:
-            st.wait_event(begin)
-        with torch.cuda.stream(streams[0]):
-            evs[0][0].record()
-            lay.swap(out_ids, host_x, zo, zo, oo, False)
-            evs[0][1].record()
-        with torch.cuda.stream(streams[1]):
-            evs[1][0].record()
-            lay.swap(host_y, in_ids, zi, zi, oi, True)
-            evs[1][1].record()
-        with torch.cuda.stream(streams[2]):
-            evs[2][0].record()
-            ops.copy_blocks(segs, csrc, cdst)
-            evs[2][1].record()
-        torch.cuda.synchronize()
-        runs.append((evs[0][0].elapsed_time(evs[0][1]) / 1e3,
-                     evs[1][0].elapsed_time(evs[1][1]) / 1e3,
-                     evs[2][0].elapsed_time(evs[2][1]) / 1e3,
-                     max(begin.elapsed_time(e[1]) for e in evs) / 1e3))
-    t_out, t_in, t_cp, span = (statistics.median(r[i] for r in runs) for i in range(4))
+        a.record(streams[2])
+        ops.copy_blocks(segs, csrc, cdst, stream=streams[2])
+        b.record(streams[2])
+        b.synchronize()
+        alone.append(a.elapsed_time(b) / 1e3)
+    t_cp_alone = statistics.median(alone)
     # correctness of everything that ran concurrently
     ok_in = all(torch.equal(t[di].view(NIN, -1).view(torch.int16).sum(dim=1, dtype=torch.int64), w)
                 for t, w in zip(segs, want_in))
@@ -569,18 +608,154 @@ def bench_overlap(args):
                    "swap_block_scale": scale, "blocks": {"d2h": NOUT, "h2d": NIN, "pairs": NP},
                    "cu_partition": ("swap streams on CUs 0-7 of each XCD, copy stream on CUs 8-31"
                                     if partition else None)},
+        "swap_workgroups": {"d2h": shared_grid[0], "h2d": shared_grid[1],
+                            "loads_per_lane": 2, "lanes": 256},
         "d2h_GBps": round(b_out / t_out / 1e9, 3),
         "h2d_GBps": round(b_in / t_in / 1e9, 3),
         "copy_blocks_GBps": round(b_cp / t_cp / 1e9, 1),
+        "copy_blocks_alone_GBps": round(b_cp / t_cp_alone / 1e9, 1),
         "link_aggregate_GBps": round((b_out + b_in) / span / 1e9, 3),
         "link_bidirectional_ceiling_GBps": round(bidir, 3),
         "frac_bidirectional_ceiling": round((b_out + b_in) / span / 1e9 / bidir, 4),
         "wall_ms": round(span * 1e3, 3),
         "per_stream_ms": {"d2h": round(t_out * 1e3, 3), "h2d": round(t_in * 1e3, 3),
-                          "copy": round(t_cp * 1e3, 3)},
+                          "copy": round(t_cp * 1e3, 3), "copy_alone": round(t_cp_alone * 1e3, 3)},
+        "default_grid": {
+            "swap_workgroups": {"d2h": default_grid[0], "h2d": default_grid[1]},
+            "d2h_GBps": round(b_out / d_out / 1e9, 3),
+            "h2d_GBps": round(b_in / d_in / 1e9, 3),
+            "copy_blocks_GBps": round(b_cp / d_cp / 1e9, 1),
+            "link_aggregate_GBps": round((b_out + b_in) / d_span / 1e9, 3),
+            "frac_bidirectional_ceiling": round((b_out + b_in) / d_span / 1e9 / bidir, 4),
+            "per_stream_ms": {"d2h": round(d_out * 1e3, 3), "h2d": round(d_in * 1e3, 3),
+                              "copy": round(d_cp * 1e3, 3)}},
         "runs": 3, "statistic": "median",
         "bit_exact": True,
     }
+
+
+def bench_copy_beside_swaps(args):
+    """An HBM-bound copy beside the swap kernels, by swap grid: copy_blocks of
+    2048 pairs of Qwen1.5-MoE tiles (48 x 64 KiB, 12.9 GB R+W) on CUs 8-31
+    of every XCD, started 25 ms into a DIRECT swap-out and/or swap-in of
+    2048 blocks (6.4 GB each, uncached pool) on CUs 0-7, for several
+    workgroup counts per swap kernel (2 loads of 16 B per lane, 8 KiB per
+    workgroup in flight). Reports each swap's rate, the copy's time and rate,
+    and with both swaps the link aggregate over their span. Medians of 2."""
+    import numpy as np
+    import torch
+
+    from aegaeon_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load()
+    L, NB, H, D, NP, NS = 24, 8192, 16, 128, 2048, 2048
+    segs = kv_segments(torch, L, NB, H, D, torch.bfloat16, dev, 4)
+    S, tile = len(segs), 16 * H * D * 2
+    page = S * tile
+    pool = ops.PinnedHostPool(2 * NS * page, uncached=True)
+    lay = ops.SegmentLayout(segs, [tile] * S, [i * tile for i in range(S)], [1] * S, NB, [1],
+                            pool.tensor, page, 0)
+    rng = np.random.default_rng(4)
+    perm = rng.permutation(NB)
+    out_ids, in_ids = perm[:NS], perm[NS:2 * NS]
+    csrc, cdst = perm[2 * NS:2 * NS + NP], perm[2 * NS + NP:2 * NS + 2 * NP]
+    hx, hy = np.arange(NS), np.arange(NS, 2 * NS)
+    z, o = np.zeros(NS, np.int32), np.ones(NS, np.int64)
+    lay.swap(in_ids, hy, z, z, o, False)
+    torch.cuda.synchronize()
+    s_out = ops.DedicatedStream(dev, ops.xcd_cu_mask(8))
+    s_in = ops.DedicatedStream(dev, ops.xcd_cu_mask(8))
+    s_cp = ops.DedicatedStream(dev, ops.xcd_cu_mask(24, 8))
+    sbytes, cbytes = NS * page, 2 * NP * S * tile
+    keys = (_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_SWAP_IN_WORKGROUPS)
+    saved = [_lib.tune(k) for k in keys]
+
+    def once(out_wg, in_wg, with_copy):
+        if out_wg:
+            _lib.tune(keys[0], out_wg)
+        if in_wg:
+            _lib.tune(keys[1], in_wg)
+        torch.cuda.synchronize()
+        begin = torch.cuda.Event(enable_timing=True)
+        begin.record()
+        ev = {}
+        for name, wg, st in (("out", out_wg, s_out.stream), ("in", in_wg, s_in.stream)):
+            if not wg:
+                continue
+            st.wait_event(begin)
+            a, b = ev_pair(torch)
+            a.record(st)
+            if name == "out":
+                lay.swap(out_ids, hx, z, z, o, False, stream=st)
+            else:
+                lay.swap(hy, in_ids, z, z, o, True, stream=st)
+            b.record(st)
+            ev[name] = (a, b)
+        if with_copy:
+            c = s_cp.stream
+            c.wait_event(begin)
+            a, b = ev_pair(torch)
+            with torch.cuda.stream(c):
+                torch.cuda._sleep(50_000_000)     # about 25 ms of shader clock
+                a.record(c)
+                ops.copy_blocks(segs, csrc, cdst, stream=c)
+                b.record(c)
+            ev["copy"] = (a, b)
+        torch.cuda.synchronize()
+        r = {k: a.elapsed_time(b) / 1e3 for k, (a, b) in ev.items()}
+        if out_wg and in_wg:
+            r["span"] = max(begin.elapsed_time(ev[k][1]) for k in ("out", "in")) / 1e3
+        return r
+
+    rows = []
+
+    def record(case, out_wg, in_wg, with_copy, reps=2):
+        rs = [once(out_wg, in_wg, with_copy) for _ in range(reps)]
+        m = {k: statistics.median(r[k] for r in rs) for k in rs[0]}
+        row = {"case": case, "swap_out_workgroups": out_wg or None,
+               "swap_in_workgroups": in_wg or None}
+        if "out" in m:
+            row["d2h_GBps"] = round(sbytes / m["out"] / 1e9, 2)
+        if "in" in m:
+            row["h2d_GBps"] = round(sbytes / m["in"] / 1e9, 2)
+        if "copy" in m:
+            row["copy_ms"] = round(m["copy"] * 1e3, 3)
+            row["copy_GBps"] = round(cbytes / m["copy"] / 1e9, 1)
+        if "span" in m:
+            row["link_aggregate_GBps"] = round(2 * sbytes / m["span"] / 1e9, 2)
+        log(json.dumps(row))
+        rows.append(row)
+
+    try:
+        record("copy alone", 0, 0, True, reps=3)
+        for w in (8, 16, 24, 32, 64, 112):
+            record("swap-out alone", w, 0, False)
+            record("copy beside swap-out", w, 0, True)
+        for w in (16, 32, 48, 64, 128):
+            record("swap-in alone", 0, w, False)
+            record("copy beside swap-in", 0, w, True)
+        for wo, wi in ((8, 16), (16, 32), (32, 64), (48, 64), (112, 128)):
+            record("both swaps", wo, wi, False)
+            record("copy beside both swaps", wo, wi, True)
+    finally:
+        for k, v in zip(keys, saved):
+            _lib.tune(k, v)
+        for st in (s_out, s_in, s_cp):
+            st.close()
+    cs, cd = torch.from_numpy(csrc).to(dev), torch.from_numpy(cdst).to(dev)
+    if not all(torch.equal(t[cd], t[cs]) for t in segs):
+        raise AssertionError("copy_blocks beside the swaps is not bit-exact")
+    del lay
+    pool.free()
+    return {"metric": "copy_blocks GB/s beside the swap kernels, by swap grid",
+            "unit": "GB/s",
+            "config": {"workload": "Qwen1.5-MoE tiles (48 x [8192,16,16,128] bf16): copy_blocks "
+                                   "of 2048 pairs on CUs 8-31 of every XCD, 25 ms into a swap-out "
+                                   "and/or swap-in of 2048 blocks on CUs 0-7",
+                       "copy_bytes_rw": cbytes, "swap_bytes_per_direction": sbytes},
+            "rows": rows, "statistic": "median of 2 (3 for the copy alone)", "bit_exact": True}
 
 
 def bench_switch(args):
@@ -628,6 +803,7 @@ def bench_switch(args):
     n_slabs = -(-sum(blocks) * page // slab) + 4
     pools = BlockPools(n_slabs, slab)
     host = ops.PinnedHostPool(n_slabs * slab, uncached=True)
+    log_pinned(ops, "with the model-switch pool")
     sw = []
     for e in range(2):
         pools.register_gpu_space(e, NB, shape, groups)
@@ -1081,6 +1257,7 @@ def main():
         sys.exit(2)
     if args.config != "headline":
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
+              "copy-beside-swaps": bench_copy_beside_swaps,
               "switch": bench_switch, "serving": bench_serving,
               "tiles": bench_tiles}[args.config]
         print(json.dumps(fn(args)), flush=True)
@@ -1096,8 +1273,9 @@ def main():
                              stdout=subprocess.PIPE, text=True, timeout=900)
         if res.returncode == 0 and res.stdout.strip():
             ov = json.loads(res.stdout.strip().splitlines()[-1])
-            overlap = {k: ov[k] for k in ("d2h_GBps", "h2d_GBps", "copy_blocks_GBps",
-                                          "link_aggregate_GBps",
+            overlap = {k: ov[k] for k in ("swap_workgroups", "d2h_GBps", "h2d_GBps",
+                                          "copy_blocks_GBps", "copy_blocks_alone_GBps",
+                                          "link_aggregate_GBps", "default_grid",
                                           "link_bidirectional_ceiling_GBps",
                                           "frac_bidirectional_ceiling", "wall_ms",
                                           "per_stream_ms", "bit_exact")}
@@ -1118,6 +1296,7 @@ def main():
     _lib.load()
 
     log("measuring host-link and stream-copy ceilings")
+    log_pinned(ops, "before the link ceilings")
     bidir, bidir_attempts = measure_link_bidir(torch, ops, dev)
     link = measure_link(torch, ops, dev)
     stream_copy = measure_stream_copy(torch, dev)
@@ -1130,6 +1309,7 @@ def main():
     S1 = len(segs1)
     tile1 = 16 * H1 * D1 * 2
     pool = ops.PinnedHostPool(HOST1 * S1 * tile1, uncached=True)
+    log_pinned(ops, "with the Qwen3-4B pool")
     g = torch.Generator().manual_seed(1)
     out_ids = (torch.randperm(NB1 - 1, generator=g)[:NSW] + 1).numpy()
     host_ids = torch.randperm(HOST1, generator=g)[:NSW].numpy()
@@ -1259,6 +1439,10 @@ def main():
             "unit": "GB/s",
             "frac": round(copy_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": (None if traffic is None else
+                               "profiles/copy_blocks_traffic.json: rocprofv3 FETCH_SIZE and "
+                               "WRITE_SIZE passes over this workload, scaled by a plain 4 GiB "
+                               "copy's counts (not measured in this run)"),
             "avg_launch_ms": round(t_cpy * 1e3, 3),
         },
         "hbm_probes": {

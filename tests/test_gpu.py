@@ -208,7 +208,7 @@ def test_prepared_layout_rejects_bad_geometry(gpu):
     with pytest.raises(ValueError, match="host tensor"):
         ops.SegmentLayout([seg], [256], [0], [1], 8, [1], seg.view(-1), 256, 0)
     lay = ops.SegmentLayout([seg], [256], [0], [1], 8, [1], pool.tensor, 256, 0)
-    with pytest.raises(ValueError, match="equal lengths"):
+    with pytest.raises(ValueError, match="unequal lengths"):
         lay.swap([1], [0], [0, 0], [0], [1], False)
     pool.free()
 
@@ -886,9 +886,9 @@ def test_rejections_enqueue_nothing(gpu):
         with pytest.raises(ValueError, match=word):
             ops.swap_segments([seg], *args, src, dst, [0] * len(src), [0] * len(src),
                               [1] * len(src), False)
-    with pytest.raises(ValueError, match="exceeds"):
+    with pytest.raises(ValueError, match="run past a page"):
         ops.swap_segments([seg], *args, [1], [0], [0], [0], [2], False)
-    with pytest.raises(ValueError, match="equal lengths"):
+    with pytest.raises(ValueError, match="unequal lengths"):
         ops.swap_segments([seg], *args, [1], [0], [0, 0], [0], [1], False)
     with pytest.raises(ValueError, match="both a source and a target"):
         ops.copy_blocks([seg], [1, 2], [2, 3])

@@ -569,9 +569,9 @@ def _swap_blocks_call(lib, *, n_seg=2, page=(4096, 4096), hoff=(0, 4096), owners
     (dict(dst=(6,)), -2, "target block id"),
     (dict(src=(1, 2), dst=(3, 3), grp=(0, 0), first=(0, 0), valid=(4, 4)), -3, "twice"),
     (dict(grp=(1,)), -2, "group id"),
-    (dict(first=(1,), valid=(4,)), -4, "exceeds page size"),
-    (dict(first=(-1,), valid=(1,)), -4, "exceeds page size"),
-    (dict(kpp=(3,)), -4, "not divisible"),
+    (dict(first=(1,), valid=(4,)), -4, "run past a page"),
+    (dict(first=(-1,), valid=(1,)), -4, "run past a page"),
+    (dict(kpp=(3,)), -4, "equal kernel blocks"),
     (dict(hoff=(0, 4097)), -2, "overruns"),
     (dict(rank_off=8192), -1, "host_rank_offset"),
     (dict(dev_blocks=1 << 62), -2, "overflows"),

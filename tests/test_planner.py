@@ -331,7 +331,7 @@ def test_cpu_allocation_waits_for_swap_ins():
 
 def test_reregistering_an_engine_settles_its_moves():
     pools, tables = _engine_with_requests(2, 4)
-    with pytest.raises(ValueError, match="still resides"):
+    with pytest.raises(ValueError, match="has blocks in it"):
         pools.register_gpu_space(0, 12, SHAPE, G1, block_tables=tables)
     out = plan_move([(0, 64), (1, 64)], tables, BLOCK_LOCATION_CPU, pools)
     pools.record_move(out, [FakeEvent()])
