@@ -538,11 +538,15 @@ CUS_PER_XCD = 32  # MI355X (gfx950): 8 XCDs of 32 CUs
 
 def xcd_cu_mask(cus_per_xcd: int, first: int = 0,
                 device: torch.device | None = None) -> list[int]:
-    """CU mask words (for DedicatedStream(cu_mask=...)) that enable CUs
-    [first, first + cus_per_xcd) of every 32-CU XCD, so the work spreads
-    over all XCDs. The runtime accepts runs of 8 or more CUs starting at a
-    multiple of 8, e.g. xcd_cu_mask(8) for the swap streams and
-    xcd_cu_mask(24, first=8) for the rest."""
+    """CU mask words (for DedicatedStream(cu_mask=...)) that give a stream
+    `cus_per_xcd` CUs on each of the 8 XCDs: mask bits i with
+    first <= i % 32 < first + cus_per_xcd. The runtime spreads every run of
+    8 consecutive mask bits over the 8 XCDs, one CU each (hardware ids read
+    by workgroups of such streams show bits 0-7 on one CU per XCD, bits 0-31
+    on four), so the CU count per XCD is what a mask sets; a mask cannot
+    confine a stream to whole XCDs. The runtime takes runs of 8 or more bits
+    starting at a multiple of 8, e.g. xcd_cu_mask(8) for the swap streams
+    and xcd_cu_mask(24, first=8) for the rest."""
     if cus_per_xcd <= 0 or first < 0 or first + cus_per_xcd > CUS_PER_XCD:
         raise ValueError(f"CUs [{first}, {first + cus_per_xcd}) do not fit a "
                          f"{CUS_PER_XCD}-CU XCD")

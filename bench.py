@@ -474,8 +474,8 @@ def bench_overlap(args):
 
     dev = torch.device("cuda:0")
     _lib.load()
-    # CU partition: the link-bound swap kernels on CUs 0-7 of every XCD, the
-    # HBM-bound copy on CUs 8-31, so the copy does not share CUs with waves
+    # CU partition: the link-bound swap kernels on 8 CUs of every XCD, the
+    # HBM-bound copy on the other 24, so the copy does not share CUs with waves
     # that wait on PCIe (without it the copy ran 150-200 ms instead of 11)
     partition = not getattr(args, "no_cu_partition", False)
     masks = ([ops.xcd_cu_mask(8, device=dev)] * 2 + [ops.xcd_cu_mask(24, 8, device=dev)]
@@ -606,7 +606,7 @@ def bench_overlap(args):
                                f"swap-in {NIN}, copy_blocks {NP} pairs, one stream each",
                    "bytes": {"d2h": b_out, "h2d": b_in, "copy_rw": b_cp},
                    "swap_block_scale": scale, "blocks": {"d2h": NOUT, "h2d": NIN, "pairs": NP},
-                   "cu_partition": ("swap streams on CUs 0-7 of each XCD, copy stream on CUs 8-31"
+                   "cu_partition": ("swap streams on 8 CUs of each XCD, copy stream on the other 24 of each XCD"
                                     if partition else None)},
         "swap_workgroups": {"d2h": shared_grid[0], "h2d": shared_grid[1],
                             "loads_per_lane": 2, "lanes": 256},
@@ -636,9 +636,9 @@ def bench_overlap(args):
 
 def bench_copy_beside_swaps(args):
     """An HBM-bound copy beside the swap kernels, by swap grid: copy_blocks of
-    2048 pairs of Qwen1.5-MoE tiles (48 x 64 KiB, 12.9 GB R+W) on CUs 8-31
-    of every XCD, started 25 ms into a DIRECT swap-out and/or swap-in of
-    2048 blocks (6.4 GB each, uncached pool) on CUs 0-7, for several
+    2048 pairs of Qwen1.5-MoE tiles (48 x 64 KiB, 12.9 GB R+W) on 24 CUs of
+    every XCD, started 25 ms into a DIRECT swap-out and/or swap-in of
+    2048 blocks (6.4 GB each, uncached pool) on the other 8, for several
     workgroup counts per swap kernel (2 loads of 16 B per lane, 8 KiB per
     workgroup in flight). Reports each swap's rate, the copy's time and rate,
     and with both swaps the link aggregate over their span. Medians of 2."""
@@ -752,8 +752,8 @@ def bench_copy_beside_swaps(args):
     return {"metric": "copy_blocks GB/s beside the swap kernels, by swap grid",
             "unit": "GB/s",
             "config": {"workload": "Qwen1.5-MoE tiles (48 x [8192,16,16,128] bf16): copy_blocks "
-                                   "of 2048 pairs on CUs 8-31 of every XCD, 25 ms into a swap-out "
-                                   "and/or swap-in of 2048 blocks on CUs 0-7",
+                                   "of 2048 pairs on 24 CUs of every XCD, 25 ms into a swap-out "
+                                   "and/or swap-in of 2048 blocks on the other 8",
                        "copy_bytes_rw": cbytes, "swap_bytes_per_direction": sbytes},
             "rows": rows, "statistic": "median of 2 (3 for the copy alone)", "bit_exact": True}
 

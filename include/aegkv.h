@@ -362,9 +362,11 @@ int aegkv_stream_release(hipStream_t stream);
  * words) enables CU i. Kernels launched on the stream run only there, so
  * link-bound swap waves can be kept off the CUs that HBM-bound work (block
  * copies, the model's kernels) uses on other streams. No counterpart in the
- * reference. The runtime accepts runs of 8 or more consecutive CUs that
- * start at a multiple of 8 (CUs are numbered 32 per XCD); it refuses finer
- * masks with a positive hipError_t status.
+ * reference. The runtime accepts runs of 8 or more consecutive mask bits
+ * that start at a multiple of 8 and refuses finer masks with a positive
+ * hipError_t status; it spreads each run of 8 bits over the 8 XCDs, one CU
+ * on each (measured from the hardware ids workgroups read), so a mask sets
+ * how many CUs of every XCD a stream gets, not which XCDs.
  */
 int aegkv_stream_create_masked(hipStream_t* stream, const uint32_t* cu_mask,
                                int32_t mask_words);

@@ -955,7 +955,7 @@ def test_runs_on_current_stream_and_orders_by_events(gpu):
 def test_swapper_block_table_round_trip(gpu, oracle, streams):
     """BlockTable.transfer_entries -> KVSwapper.swap_blocks out and back in,
     partial extents included, checked against the oracle; on torch pool
-    streams, dedicated streams, dedicated streams on CUs 0-7 of every XCD,
+    streams, dedicated streams, dedicated streams on 8 CUs of every XCD,
     and with the swapper's default mode set to STAGED."""
     from aegaeon_amd.cache_groups import BlockTable, CacheGroupConfig, CacheGroupRuntimeConfig
     from aegaeon_amd.layout import KVCacheTensorSpec, allocate_composite_cache
@@ -1488,8 +1488,8 @@ def test_dedicated_stream_lives_with_its_torch_stream(gpu):
 
 
 def test_swaps_and_copy_on_cu_partitioned_streams(gpu):
-    """Swap streams on CUs 0-7 of every XCD and a copy_blocks stream on CUs
-    8-31, running at once: every block lands where the closed form says."""
+    """Swap streams on 8 CUs of every XCD and a copy_blocks stream on the
+    other 24, running at once: every block lands where the closed form says."""
     swap_mask = ops.xcd_cu_mask(8)
     copy_mask = ops.xcd_cu_mask(24, first=8)
     assert all(a & b == 0 for a, b in zip(swap_mask, copy_mask))
