@@ -82,6 +82,9 @@ def parse():
     p.add_argument("--no-reference-loop", action="store_true",
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
+    p.add_argument("--overlap-workgroups", default="16,16",
+                   help="overlap config: swap-out,swap-in workgroups of its first run "
+                        "(the second always uses the library's defaults)")
     p.add_argument("--config", default="headline",
                    choices=["headline", "varlen", "overlap", "refplan", "switch", "serving",
                             "tiles", "copy-beside-swaps"],
@@ -532,7 +535,11 @@ def bench_overlap(args):
     streams = [o.stream for o in owners]
     grid_keys = (_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_SWAP_IN_WORKGROUPS)
     default_grid = tuple(_lib.tune(k) for k in grid_keys)
-    shared_grid = (16, 16)
+    shared_grid = tuple(int(x) for x in
+                        getattr(args, "overlap_workgroups", "16,16").split(","))
+    if len(shared_grid) != 2 or min(shared_grid) <= 0:
+        raise ValueError(f"--overlap-workgroups takes two counts above zero, "
+                         f"not {args.overlap_workgroups!r}")
 
     def three_streams(grid):
         for k, v in zip(grid_keys, grid):
@@ -736,7 +743,8 @@ def bench_copy_beside_swaps(args):
         for w in (16, 32, 48, 64, 128):
             record("swap-in alone", 0, w, False)
             record("copy beside swap-in", 0, w, True)
-        for wo, wi in ((8, 16), (16, 32), (32, 64), (48, 64), (112, 128)):
+        for wo, wi in ((8, 16), (16, 16), (16, 32), (24, 24), (24, 32), (32, 32), (32, 64),
+                       (48, 64), (112, 128)):
             record("both swaps", wo, wi, False)
             record("copy beside both swaps", wo, wi, True)
     finally:
