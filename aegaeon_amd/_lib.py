@@ -47,6 +47,7 @@ TUNE_STAGED_WORKGROUPS = 13
 TUNE_STAGED_OVERLAP = 14
 TUNE_SWAP_OUT_WORKGROUPS_UNCACHED = 15
 TUNE_COPY_LANES = 17
+TUNE_COPY_ORDER = 18
 HOST_UNCACHED = 1
 HOST_COHERENT = 2
 PROBE_READ = 1

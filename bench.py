@@ -433,14 +433,29 @@ def bench_tiles(args):
         n = blocks // 2
         src, dst = perm[:n], perm[n:2 * n]
         nbytes = n * len(segs) * tile
-        ops.copy_blocks(segs, src, dst)
-        a, b = ev_pair(torch)
-        a.record()
-        for _ in range(args.steps):
+
+        def timed():
             ops.copy_blocks(segs, src, dst)
-        b.record()
-        b.synchronize()
-        t = a.elapsed_time(b) / 1e3 / args.steps
+            a, b = ev_pair(torch)
+            a.record()
+            for _ in range(args.steps):
+                ops.copy_blocks(segs, src, dst)
+            b.record()
+            b.synchronize()
+            return a.elapsed_time(b) / 1e3 / args.steps
+
+        # the library's pair orders side by side (3 interleaved rounds,
+        # medians): as given, by target id (the default), by source id
+        default_order = _lib.tune(_lib.TUNE_COPY_ORDER)
+        by_order = {o: [] for o in (0, 1, 2)}
+        try:
+            for _ in range(3):
+                for o in by_order:
+                    _lib.tune(_lib.TUNE_COPY_ORDER, o)
+                    by_order[o].append(timed())
+        finally:
+            _lib.tune(_lib.TUNE_COPY_ORDER, default_order)
+        t = statistics.median(by_order[default_order])
         si, di = torch.from_numpy(src).to(dev), torch.from_numpy(dst).to(dev)
         if not all(torch.equal(x[di], x[si]) for x in segs):
             raise AssertionError(f"{name}: copy_blocks is not bit-exact")
@@ -449,6 +464,9 @@ def bench_tiles(args):
         rows.append({"shape": name, "tile_bytes": tile, "segments": len(segs), "pairs": n,
                      "bytes_rw": 2 * nbytes, "copy_ms": round(t * 1e3, 3),
                      "copy_GBps": round(copy, 1), "copy_frac_hbm_peak": round(copy / HBM_PEAK_GBPS, 4),
+                     "copy_GBps_by_pair_order": {
+                         k: round(2 * nbytes / statistics.median(by_order[o]) / 1e9, 1)
+                         for k, o in (("as_given", 0), ("by_target", 1), ("by_source", 2))},
                      "read_GBps": round(pr["read"], 1), "write_GBps": round(pr["write"], 1),
                      "rw_bound_GBps": round(pr["rw_bound"], 1),
                      "copy_frac_of_rw_bound": round(copy / pr["rw_bound"], 4)})

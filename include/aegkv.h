@@ -106,6 +106,10 @@ extern "C" {
                                         7): 256 or 1024 lanes per workgroup
                                         (0 = 1024; 256 lanes take an unroll
                                         of 1, 2, 4 or 8)                   */
+#define AEGKV_TUNE_COPY_ORDER 18     /* copy_blocks: pairs reach the kernel
+                                        as given (0), sorted by target id
+                                        (1, default) or by source id (2);
+                                        the result does not depend on it   */
 
 /* ABI version of the loaded library (AEGKV_ABI_VERSION). */
 int aegkv_abi_version(void);

@@ -7,6 +7,8 @@ before any other GPU test has pinned memory, and the swaps get the largest
 scale the host allows (3/4 on these hosts, as in bench.py --config overlap).
 """
 
+import warnings
+
 import numpy as np
 import pytest
 import torch
@@ -110,22 +112,25 @@ def test_qwen15_moe_three_streams_at_config_size(gpu):
         ops.copy_blocks(segs, csrc, cdst)
     torch.cuda.synchronize()
     _say(f"three streams took {time.perf_counter() - t1:.2f} s")
+    at = f"c4 at swap scale {scale} ({NOUT} out, {NIN} in)"
     moved = np.zeros(NB, bool)
     moved[cdst] = True
     keep = torch.from_numpy(~moved).to(gpu)
     dcs, dcd = torch.from_numpy(csrc).to(gpu), torch.from_numpy(cdst).to(gpu)
     for s_, t in enumerate(segs):
         now = sums(t)
-        assert torch.equal(now[:, keep], before[s_][:, keep]), s_   # swap-in targets included
-        assert torch.equal(t[dcd], t[dcs]), s_
+        assert torch.equal(now[:, keep], before[s_][:, keep]), (at, s_)   # swap-in targets too
+        assert torch.equal(t[dcd], t[dcs]), (at, s_)
     pages = pool.tensor.view(NOUT + NIN, S, tile)
     for k in rng.choice(NOUT, 48, replace=False):
         got = pages[int(hx[k])].to(gpu)
         want = torch.stack([t[int(out_ids[k])].reshape(-1).view(torch.uint8) for t in segs])
-        assert torch.equal(got, want), int(k)
+        assert torch.equal(got, want), (at, int(k))
     del lay, pages
     pool.free()
     del segs, before, w
     torch.cuda.empty_cache()      # the 96 GiB cache goes before the other GPU tests
     _say(f"c4 test done in {time.perf_counter() - t0:.1f} s at swap scale {scale} "
          f"({NOUT} out, {NIN} in)")
+    if scale < 1.0:   # shown in the run's summary even when the test passes
+        warnings.warn(f"{at}: the host pins less than the config's 84 GiB of pages")

@@ -369,7 +369,7 @@ def restore_tuning():
             _lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_IN_WORKGROUPS, _lib.TUNE_NT_STORES,
             _lib.TUNE_STAGED_DMA_STREAMS, _lib.TUNE_STAGING_BYTES, _lib.TUNE_COPY_LDS_BYTES,
             _lib.TUNE_SWAP_UNROLL, _lib.TUNE_STAGED_WORKGROUPS, _lib.TUNE_STAGED_OVERLAP,
-            _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_COPY_LANES)
+            _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, _lib.TUNE_COPY_LANES, _lib.TUNE_COPY_ORDER)
     saved = {k: _lib.tune(k) for k in keys}
     yield
     for k, v in saved.items():
@@ -431,6 +431,41 @@ def test_copy_blocks_every_shape_vs_oracle(gpu, oracle, restore_tuning):
         torch.cuda.synchronize()
         for s in range(4):
             assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (lanes, unroll, wpc, lds, s)
+
+
+@pytest.mark.parametrize("order", [0, 1, 2])
+def test_copy_blocks_pair_orders_vs_oracle(gpu, oracle, restore_tuning, order):
+    """The library may hand the kernel the pairs in the caller's order, by
+    target id or by source id (a counting sort, one pass per byte of the
+    largest id): every order gives the oracle's bytes, for ids of one, two
+    and three bytes, pairs already in order, one pair, and the
+    allocation-free copy."""
+    _lib.tune(_lib.TUNE_COPY_ORDER, order)
+    rng = np.random.default_rng(70 + order)
+    page = 4096
+    for n_blocks, n in ((200, 60), (5000, 1500), (70000, 300), (70000, 1), (3000, 1000)):
+        segs_np = [rng.integers(0, 256, (n_blocks, page // 2), dtype=np.uint8) for _ in range(2)]
+        perm = rng.permutation(n_blocks)
+        src, dst = perm[:n], perm[n:2 * n]
+        if n_blocks == 3000:                      # already in order of both ids
+            src, dst = np.sort(src), np.sort(dst)
+        segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+        ops.copy_blocks(segs, src, dst)
+        oracle.copy_blocks([x.reshape(-1) for x in segs_np], np.array([page // 2] * 2, np.int64),
+                           n_blocks, src, dst)
+        torch.cuda.synchronize()
+        for s in range(2):
+            assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (order, n_blocks, n, s)
+    segs_np = [rng.integers(0, 256, (900, 1024), dtype=np.uint8) for _ in range(3)]
+    perm = rng.permutation(900)
+    src, dst = perm[:400], perm[400:800]
+    segs = [torch.from_numpy(x.copy()).to(gpu) for x in segs_np]
+    ops.copy_blocks_noalloc(segs, src, dst)
+    oracle.copy_blocks([x.reshape(-1) for x in segs_np], np.array([1024] * 3, np.int64), 900,
+                       src, dst)
+    torch.cuda.synchronize()
+    for s in range(3):
+        assert np.array_equal(segs[s].cpu().numpy(), segs_np[s]), (order, "noalloc", s)
 
 
 @pytest.mark.parametrize("shape_auto,unroll", [(0, 4), (0, 2), (0, 1), (1, 4)])

@@ -521,6 +521,11 @@ def test_tuning_knobs(aegkv_lib):
     assert _lib.tune(_lib.TUNE_COPY_LANES, 0) == 256
     with pytest.raises(ValueError, match="unknown tuning key 16"):
         _lib.tune(16)          # the retired library-driven DMA key
+    assert _lib.tune(_lib.TUNE_COPY_ORDER) == 1              # by target id
+    with pytest.raises(ValueError, match="copy order"):
+        _lib.tune(_lib.TUNE_COPY_ORDER, 3)
+    assert _lib.tune(_lib.TUNE_COPY_ORDER, 2) == 1
+    assert _lib.tune(_lib.TUNE_COPY_ORDER, 1) == 2
     with pytest.raises(ValueError):
         _lib.tune(_lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED, 0)
     with pytest.raises(ValueError):
