@@ -1456,6 +1456,7 @@ def main():
             "pairs_per_s": round(NP / t_cpy, 1),
             "frac_hbm_peak": round(copy_gbps / HBM_PEAK_GBPS, 4),
             "stream_copy_ceiling_GBps": round(stream_copy, 1),
+            "pair_order": ("as_given", "by_target", "by_source")[_lib.tune(_lib.TUNE_COPY_ORDER)],
         },
         "roofline": {
             "bound": "hbm",
