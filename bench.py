@@ -82,6 +82,10 @@ def parse():
     p.add_argument("--no-reference-loop", action="store_true",
                    help="skip timing the reference per-extent copy loop on the GPU "
                         "(about 147k copy_ calls; very slow under a memory-copy trace)")
+    p.add_argument("--swap-workgroups", default=None,
+                   help="OUT,IN: swap-out (cached and uncached pools) and swap-in "
+                        "workgroups for this process's swaps instead of the library's "
+                        "defaults (the overlap child keeps --overlap-workgroups)")
     p.add_argument("--overlap-workgroups", default="16,16",
                    help="overlap config: swap-out,swap-in workgroups of its first run "
                         "(the second always uses the library's defaults)")
@@ -1272,6 +1276,20 @@ def bench_refplan(args):
     }
 
 
+def apply_swap_workgroups(args):
+    """--swap-workgroups OUT,IN: this process's swap grids (loads the
+    library, so it runs after any child process has been started)."""
+    if not args.swap_workgroups:
+        return
+    from aegaeon_amd import _lib
+
+    out_wg, in_wg = (int(x) for x in args.swap_workgroups.split(","))
+    for key in (_lib.TUNE_SWAP_OUT_WORKGROUPS, _lib.TUNE_SWAP_OUT_WORKGROUPS_UNCACHED):
+        _lib.tune(key, out_wg)
+    _lib.tune(_lib.TUNE_SWAP_IN_WORKGROUPS, in_wg)
+    log(f"swap workgroups set to {out_wg} out, {in_wg} in")
+
+
 def main():
     # a crash in native code prints the Python stack of every thread
     faulthandler.enable()
@@ -1282,6 +1300,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
     if args.config != "headline":
+        apply_swap_workgroups(args)
         fn = {"varlen": bench_varlen, "overlap": bench_overlap, "refplan": bench_refplan,
               "copy-beside-swaps": bench_copy_beside_swaps,
               "switch": bench_switch, "serving": bench_serving,
@@ -1311,6 +1330,7 @@ def main():
             overlap["process"] = "bench.py --config overlap, a child process run first"
         else:
             overlap = {"error": f"bench.py --config overlap exited with {res.returncode}"}
+    apply_swap_workgroups(args)   # after the child: this process touches the GPU from here
 
     import numpy as np
     import torch
