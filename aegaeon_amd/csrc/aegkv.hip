@@ -2257,6 +2257,11 @@ int aegkv_host_alloc_flags(void** ptr, int64_t bytes, int flags) {
   if (!ptr || bytes <= 0) return fail(AEGKV_EINVAL, "host_alloc needs a pointer and bytes > 0");
   if (flags & ~(AEGKV_HOST_UNCACHED | AEGKV_HOST_COHERENT))
     return fail(AEGKV_EINVAL, "unknown host_alloc flags 0x%x", flags);
+  // hipHostMalloc refuses the pair; uncached memory bypasses every cache
+  // already, and COHERENT is meant for cached pools
+  if ((flags & AEGKV_HOST_UNCACHED) && (flags & AEGKV_HOST_COHERENT))
+    return fail(AEGKV_EINVAL, "AEGKV_HOST_UNCACHED and AEGKV_HOST_COHERENT do not combine "
+                "(uncached memory is coherent already)");
   const size_t n = static_cast<size_t>(bytes);
   const bool uncached = (flags & AEGKV_HOST_UNCACHED) != 0;
   unsigned hf = hipHostMallocMapped | hipHostMallocPortable;

@@ -400,7 +400,9 @@ int aegkv_host_alloc(void** ptr, int64_t bytes);
  * cap on pinned memory. Meant for long-lived pools such as a KV host pool.
  * AEGKV_HOST_COHERENT allocates fine-grained coherent memory
  * (hipHostMallocCoherent), for words both the GPU and the host write and
- * read while kernels run, such as move guards.
+ * read while kernels run, such as move guards. The two flags do not
+ * combine (AEGKV_EINVAL: hipHostMalloc refuses the pair, and uncached
+ * memory is coherent already).
  */
 #define AEGKV_HOST_UNCACHED 1
 #define AEGKV_HOST_COHERENT 2

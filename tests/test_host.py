@@ -782,6 +782,9 @@ def test_host_alloc_flags_rejections(aegkv_lib):
     assert b"flags" in aegkv_lib.aegkv_last_error()
     assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 0, 1) == _lib.EINVAL
     assert aegkv_lib.aegkv_host_alloc_flags(None, 16, 1) == _lib.EINVAL
+    both = _lib.HOST_UNCACHED | _lib.HOST_COHERENT      # hipHostMalloc refuses the pair
+    assert aegkv_lib.aegkv_host_alloc_flags(ctypes.byref(p), 4096, both) == _lib.EINVAL
+    assert b"do not combine" in aegkv_lib.aegkv_last_error()
     assert aegkv_lib.aegkv_host_free(ctypes.c_void_p(0x1000)) == _lib.EINVAL   # not a pool
     assert b"live pool" in aegkv_lib.aegkv_last_error()
 
