@@ -186,3 +186,59 @@ def test_guard_merge_and_guarded_signal(gpu):
         torch.cuda.synchronize()
         st.close()
         hw.close()
+
+
+@pytest.mark.parametrize("mode", ["direct", "staged"])
+def test_guarded_swaps_in_both_modes(gpu, mode):
+    """A set guard stops a swap in either transfer mode: a swap-in moves
+    nothing into the cache (STAGED: the scatter kernel reads the guard; the
+    runtime's copies into staging still run); a swap-out leaves the cache
+    alone (DIRECT: the host pages too). With the guard clear, the same
+    calls move the blocks."""
+    _say(f"guarded swaps, {mode}")
+    n_seg, n_blocks, tile = 4, 32, 16 * 1024
+    g = torch.Generator(device=gpu).manual_seed(41)
+    segs = [torch.empty(n_blocks, tile, dtype=torch.uint8, device=gpu) for _ in range(n_seg)]
+    for t in segs:
+        t.view(torch.int32).random_(generator=g)
+    page = n_seg * tile
+    pool = ops.PinnedHostPool(8 * page)
+    host = pool.tensor.view(8, n_seg, tile)
+    host.view(torch.int32).random_()
+    lay = ops.SegmentLayout(segs, [tile] * n_seg, [s * tile for s in range(n_seg)], [1] * n_seg,
+                            n_blocks, [1], pool.tensor, page, 0)
+    guards = ops.GuardWords(1)
+    st = ops.DedicatedStream(gpu)
+    z, f, o = np.zeros(3, np.int32), np.zeros(3, np.int64), np.ones(3, np.int64)
+    try:
+        before_dev = [t.clone() for t in segs]
+        before_host = host.clone()
+        guards.tensor[0] = 1
+        lay.swap([0, 1, 2], [5, 6, 7], z, f, o, True, mode=mode, stream=st.stream,
+                 guard=guards.tensor)
+        lay.swap([8, 9, 10], [3, 4, 5], z, f, o, False, mode=mode, stream=st.stream,
+                 guard=guards.tensor)
+        st.stream.synchronize()
+        for a, b in zip(segs, before_dev):
+            assert torch.equal(a, b), "a guarded swap changed the cache"
+        if mode == "direct":
+            assert torch.equal(host, before_host), "a guarded swap-out wrote host pages"
+        else:   # STAGED swap-out pages are undefined; only the untouched ones are checked
+            for h in (0, 1, 2, 6, 7):
+                assert torch.equal(host[h], before_host[h]), h
+        guards.tensor[0] = 0
+        lay.swap([0, 1, 2], [5, 6, 7], z, f, o, True, mode=mode, stream=st.stream,
+                 guard=guards.tensor)
+        lay.swap([8, 9, 10], [3, 4, 5], z, f, o, False, mode=mode, stream=st.stream,
+                 guard=guards.tensor)
+        st.stream.synchronize()
+        for s in range(n_seg):
+            for h, d in ((0, 5), (1, 6), (2, 7)):
+                assert torch.equal(segs[s][d].cpu(), host[h, s]), (s, h, d)
+            for d, h in ((8, 3), (9, 4), (10, 5)):
+                assert torch.equal(host[h, s], segs[s][d].cpu()), (s, d, h)
+    finally:
+        torch.cuda.synchronize()
+        st.close()
+    del lay, host
+    pool.free()
